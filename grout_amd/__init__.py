@@ -1,0 +1,268 @@
+"""grout_amd — MI355X-native Qwen3 attention hot path of NikVisel/grout.
+
+The product is the C-ABI library ``libgrout_attn_hip.so`` (hand-written HIP for
+gfx950, declared in ``include/grout_attn_hip.h``).  This package is the host-side
+mirror of grout's operator interface for that path, the same names, argument
+meaning and error behaviour as the Rust call sites it replaces:
+
+=====================================  ==========================================
+grout (Rust, src/)                     here
+=====================================  ==========================================
+build_inv_freq (model.rs:5992)         :func:`build_inv_freq`
+execute_qk_norm_rope_kv_prefill_op_ctx :func:`qk_norm_rope_kv_prefill`
+  (model.rs:4463)
+qk_norm_rope_kv_decode_raw_f16 record  :func:`qk_norm_rope_kv_decode`
+  (model.rs:3194)
+attend_seq_arc_into_ctx_with_position  :func:`attend_prefill`
+  (model.rs:5556), Host position
+fmha_decode_gqa_split record           :func:`fmha_decode_gqa_split`
+  (model.rs:3428)
+splitk_reduce_merge record             :func:`splitk_reduce_merge`
+  (model.rs:3453)
+DecodeCudaGraphRunner (model.rs:318)   :class:`DecodeGraphRunner`
+=====================================  ==========================================
+
+Tensors are torch tensors on the GPU (PyTorch is plumbing for device memory and
+streams here); every op launches on ``torch.cuda.current_stream()``.  Shape
+checks raise :class:`GroutError` with the reference's ``ensure!`` message before
+anything is launched; a non-zero status from the library also raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+from . import _lib
+from ._lib import GROUT_OK, LibraryMissing
+
+__all__ = [
+    "GroutError", "LibraryMissing", "lib", "build_inv_freq", "qk_norm_rope_kv_prefill",
+    "qk_norm_rope_kv_decode", "attend_prefill", "fmha_decode_gqa_split",
+    "splitk_reduce_merge", "decode_scratch", "pick_num_splits", "DecodeGraphRunner",
+    "HEAD_DIM", "ATTN_BN_DECODE",
+]
+
+HEAD_DIM = 128
+# src/model.rs:128 ATTN_BN_DECODE: KV tile of the decode split boundaries.
+ATTN_BN_DECODE = 32
+
+
+class GroutError(RuntimeError):
+    """A rejected argument (reference ``ensure!``) or a failed launch."""
+
+    def __init__(self, message: str, status: int | None = None):
+        super().__init__(message)
+        self.status = status
+
+
+def lib():
+    return _lib.load()
+
+
+def _check(status: int, what: str):
+    if status != GROUT_OK:
+        text = lib().grout_status_string(status).decode()
+        name = _lib.STATUS_NAMES.get(status, f"hipError {status}")
+        raise GroutError(f"{what}: {name} ({text})", status)
+
+
+def _ensure(cond: bool, msg: str):
+    if not cond:
+        raise GroutError(msg)
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _ptr(t) -> int:
+    return t.data_ptr()
+
+
+def _stream() -> int:
+    torch = _torch()
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _f16(t, name: str):
+    torch = _torch()
+    _ensure(t.dtype == torch.float16, f"{name} must be f16, got {t.dtype}")
+    _ensure(t.is_cuda, f"{name} must be a device tensor")
+    _ensure(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def build_inv_freq(theta: float, head_dim: int = HEAD_DIM):
+    """src/model.rs:5992-6003 on the host (f32); returns a CPU float32 tensor."""
+    torch = _torch()
+    out = (ctypes.c_float * (head_dim // 2))()
+    _check(lib().grout_build_inv_freq(float(theta), head_dim, out), "build_inv_freq")
+    return torch.tensor(list(out), dtype=torch.float32)
+
+
+def qk_norm_rope_kv_prefill(q, k, v, q_weight, k_weight, inv_freq, out, k_cache, v_cache,
+                            eps: float, position_start: int):
+    """execute_qk_norm_rope_kv_prefill_op_ctx (src/model.rs:4463-4598).
+
+    q [S,Hq,D], k/v [S,Hkv,D], out [S,Hq,D]; writes cache rows
+    [position_start, position_start+S) of k_cache/v_cache [Hkv,MS,D]."""
+    _ensure(q.dim() == 3, f"q shape mismatch in fused qk/rope/kv prefill: {list(q.shape)}")
+    S, Hq, D = q.shape
+    _ensure(k.dim() == 3 and k.shape[0] == S and k.shape[2] == D,
+            f"k shape mismatch in fused qk/rope/kv prefill: {list(k.shape)}")
+    Hkv = k.shape[1]
+    _ensure(list(v.shape) == [S, Hkv, D],
+            f"v shape mismatch in fused qk/rope/kv prefill: {list(v.shape)}")
+    _ensure(list(out.shape) == [S, Hq, D],
+            f"fused qk/rope/kv output shape mismatch: {list(out.shape)}")
+    _ensure(D % 2 == 0, f"fused qk/rope/kv requires even head_dim, got {D}")
+    MS = k_cache.shape[1] if k_cache.dim() == 3 else -1
+    _ensure(position_start + S <= MS,
+            f"fused qk/rope/kv range [{position_start}..{position_start + S}) exceeds "
+            f"max_seq_len {MS}")
+    _ensure(list(k_cache.shape) == [Hkv, MS, D],
+            f"k_cache shape mismatch in fused qk/rope/kv: {list(k_cache.shape)}")
+    _ensure(list(v_cache.shape) == [Hkv, MS, D],
+            f"v_cache shape mismatch in fused qk/rope/kv: {list(v_cache.shape)}")
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (q_weight, "q_weight"), (k_weight, "k_weight"),
+                 (out, "out"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _f16(t, n)
+    _check(lib().grout_qk_norm_rope_kv_prefill(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(q_weight), _ptr(k_weight), _ptr(inv_freq), _ptr(out),
+        _ptr(k_cache), _ptr(v_cache), float(eps), int(position_start), S, Hq, Hkv, D, MS,
+        _stream()), "qk_norm_rope_kv_prefill")
+    return out
+
+
+def qk_norm_rope_kv_decode(qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache,
+                           position, eps: float, num_q_heads: int, num_kv_heads: int):
+    """qk_norm_rope_kv_decode_raw_f16 as recorded at src/model.rs:3194-3221.
+
+    ``position`` is a device u32 tensor of shape [1] (torch.int32 storage)."""
+    D = q_weight.shape[0]
+    _ensure(qkv.numel() == (num_q_heads + 2 * num_kv_heads) * D,
+            f"qkv has {qkv.numel()} elements, expected {(num_q_heads + 2 * num_kv_heads) * D}")
+    _ensure(q_out.numel() >= num_q_heads * D, "q_out too small")
+    _ensure(position.numel() == 1,
+            f"attention position tensor must be shape [1], got {list(position.shape)}")
+    MS = k_cache.shape[1]
+    _check(lib().grout_qk_norm_rope_kv_decode(
+        _ptr(qkv), _ptr(q_weight), _ptr(k_weight), _ptr(inv_freq), _ptr(q_out), _ptr(k_cache),
+        _ptr(v_cache), _ptr(position), float(eps), num_q_heads, num_kv_heads, D, MS,
+        _stream()), "qk_norm_rope_kv_decode")
+
+
+def attend_prefill(q, k_cache, v_cache, out, position_start: int,
+                   qk_scale: float | None = None, kv_len: int | None = None):
+    """attend_seq_arc_into_ctx_with_position with a host position (src/model.rs:5556-5834).
+
+    kv_len defaults to position_start + q_len (:5638); qk_scale to 1/sqrt(D) in
+    f32 (:5601)."""
+    _ensure(q.dim() == 3, f"q must be rank 3 [seqlen, heads, head_dim], got {list(q.shape)}")
+    q_len, Hq, D = q.shape
+    Hkv, MS, _ = k_cache.shape
+    _ensure(list(out.shape) == [q_len, Hq, D],
+            f"attend output shape mismatch, got {list(out.shape)}")
+    if qk_scale is None:
+        qk_scale = 1.0 / math.sqrt(float(D))
+    if kv_len is None:
+        kv_len = position_start + q_len
+    for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out")):
+        _f16(t, n)
+    _check(lib().grout_attn_prefill(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), float(qk_scale), Hq, Hkv, D, q_len,
+        int(kv_len), int(position_start), MS, _stream()), "attn_prefill")
+    return out
+
+
+def pick_num_splits(max_context: int, num_kv_heads: int, block_n: int = ATTN_BN_DECODE,
+                    device: int | None = None) -> int:
+    torch = _torch()
+    cu = ctypes.c_int32(0)
+    dev = torch.cuda.current_device() if device is None else device
+    _check(lib().grout_device_cu_count(dev, ctypes.byref(cu)), "device_cu_count")
+    return int(lib().grout_attn_decode_pick_splits(cu.value, num_kv_heads, max_context,
+                                                   block_n))
+
+
+def decode_scratch(num_kv_heads: int, group: int, num_splits: int, head_dim: int = HEAD_DIM,
+                   device="cuda"):
+    """Split-K scratch (src/model.rs:2508-2525): att [Hkv, NKS*G, D] f16, lse [Hkv, NKS*G] f32."""
+    torch = _torch()
+    att = torch.zeros((num_kv_heads, num_splits * group, head_dim), dtype=torch.float16,
+                      device=device)
+    lse = torch.zeros((num_kv_heads, num_splits * group), dtype=torch.float32, device=device)
+    return att, lse
+
+
+def fmha_decode_gqa_split(q_grouped, k_cache, v_cache, att_partial, lse_partial,
+                          qk_scale_f16_bits: int, position, block_n: int = ATTN_BN_DECODE):
+    """fmha_decode_gqa_split as recorded at src/model.rs:3428-3452; q_grouped [Hkv, G, D]."""
+    Hkv, G, D = q_grouped.shape
+    _ensure(att_partial.dim() == 3 and att_partial.shape[0] == Hkv
+            and att_partial.shape[1] % G == 0, "att_partial shape mismatch")
+    ns = att_partial.shape[1] // G
+    _ensure(list(lse_partial.shape) == [Hkv, ns * G], "lse_partial shape mismatch")
+    _check(lib().grout_attn_decode_split(
+        _ptr(q_grouped), _ptr(k_cache), _ptr(v_cache), _ptr(att_partial), _ptr(lse_partial),
+        int(qk_scale_f16_bits), _ptr(position), Hkv, G, D, k_cache.shape[1], block_n, ns,
+        _stream()), "fmha_decode_gqa_split")
+
+
+def splitk_reduce_merge(att_partial, lse_partial, out):
+    """splitk_reduce_merge as recorded at src/model.rs:3453-3473; out [Hkv, G, D]."""
+    Hkv, G, D = out.shape
+    ns = att_partial.shape[1] // G
+    _check(lib().grout_attn_decode_merge(
+        _ptr(att_partial), _ptr(lse_partial), _ptr(out), Hkv, G, D, ns, _stream()),
+        "splitk_reduce_merge")
+    return out
+
+
+class DecodeGraphRunner:
+    """Attention slice of DecodeCudaGraphRunner (src/model.rs:318-493).
+
+    Captures {fused norm/RoPE/KV write, split-K decode, merge} for one layer's
+    buffers into a hipGraph; :meth:`launch_step` rewrites the device position
+    and replays it (no host sync)."""
+
+    def __init__(self, *, qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache,
+                 att_partial, lse_partial, attn_out, position, eps: float,
+                 qk_scale_f16_bits: int, num_q_heads: int, num_kv_heads: int,
+                 num_splits: int, block_n: int = ATTN_BN_DECODE, prime_position: int = 0,
+                 stream=None):
+        torch = _torch()
+        self._keep = (qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache, att_partial,
+                      lse_partial, attn_out, position)
+        self.stream = stream if stream is not None else torch.cuda.Stream()
+        L = _lib.DecodeLayer(
+            qkv=_ptr(qkv), q_weight=_ptr(q_weight), k_weight=_ptr(k_weight),
+            inv_freq=_ptr(inv_freq), q_out=_ptr(q_out), k_cache=_ptr(k_cache),
+            v_cache=_ptr(v_cache), att_partial=_ptr(att_partial),
+            lse_partial=_ptr(lse_partial), attn_out=_ptr(attn_out),
+            d_position=_ptr(position), eps=float(eps), qk_scale_f16=int(qk_scale_f16_bits),
+            num_q_heads=num_q_heads, num_kv_heads=num_kv_heads, head_dim=q_weight.shape[0],
+            max_seq_len=k_cache.shape[1], block_n=block_n, num_splits=num_splits)
+        self._layer = L
+        h = ctypes.c_void_p()
+        _check(lib().grout_decode_runner_create(ctypes.byref(L), int(prime_position),
+                                                self.stream.cuda_stream, ctypes.byref(h)),
+               "decode_runner_create")
+        self._h = h
+
+    def launch_step(self, position: int):
+        _check(lib().grout_decode_runner_step(self._h, int(position)), "decode_runner_step")
+
+    def zero_kv_caches(self):
+        _check(lib().grout_decode_runner_zero_kv(self._h), "decode_runner_zero_kv")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _check(lib().grout_decode_runner_destroy(self._h), "decode_runner_destroy")
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,230 @@
+/*
+ * grout_attn_hip.h — C ABI of the MI355X (gfx950) Qwen3 attention hot path.
+ *
+ * Drop-in for the attention ops of NikVisel/grout's Qwen3Engine: the fused
+ * per-head Q/K RMSNorm + RoPE + KV-cache write, causal flash-attention
+ * prefill, split-K GQA decode and its merge, and the hipGraph replay of the
+ * decode step.  Every kernel is hand-written HIP for CDNA4; nothing here is
+ * generated from the reference's cuTile code.
+ *
+ * Calling rules (all entry points):
+ *  - Return int32_t: 0 = GROUT_OK, < 0 = argument validation failed (one
+ *    code per reference `ensure!`, see grout_status_string), > 0 = the
+ *    hipError_t of a failed launch.
+ *  - Tensor pointers are borrowed device memory; f16 tensors are IEEE
+ *    binary16 (passed as uint16_t*).  Every pointer must be 16-byte aligned.
+ *  - Nothing is allocated or freed and nothing synchronises the host: every
+ *    launch is asynchronous on `stream` (NULL = the default stream), so the
+ *    decode entry points can be recorded into a hipGraph and replayed.
+ *  - Functions are reentrant; kernels are compiled into this library.
+ *  - Layouts are grout's: KV cache [num_kv_heads, max_seq_len, head_dim] f16
+ *    row-major (src/model.rs:1450-1455); prefill Q/O [seq, num_q_heads,
+ *    head_dim]; decode Q = the first num_q_heads*head_dim elements of q_out,
+ *    viewed [num_kv_heads, group, head_dim]; decode out [num_kv_heads, group,
+ *    head_dim] (== [1, num_q_heads, head_dim]).  head_dim must be 128, as
+ *    grout's engine requires (src/model.rs:1327).
+ *
+ * Citations are to files of the upstream NikVisel/grout tree.
+ */
+#ifndef GROUT_ATTN_HIP_H
+#define GROUT_ATTN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as hipStream_t (struct ihipStream_t*), declared without HIP headers. */
+typedef struct ihipStream_t* grout_stream_t;
+
+/* ----------------------------------------------------------- status codes */
+enum {
+    GROUT_OK = 0,
+    GROUT_ERR_NULL_POINTER = -1,  /* a required pointer is NULL */
+    GROUT_ERR_ALIGNMENT = -2,     /* a tensor pointer is not 16-byte aligned */
+    GROUT_ERR_HEAD_DIM = -3,      /* head_dim != 128 (src/model.rs:1327, :4520-4524) */
+    GROUT_ERR_HEADS = -4,         /* heads <= 0 or num_q_heads % num_kv_heads != 0 */
+    GROUT_ERR_SEQ_RANGE = -5,     /* position_start + seq_len > max_seq_len (src/model.rs:4525-4531) */
+    GROUT_ERR_KV_LEN = -6,        /* kv_len / query_start / q_len out of range */
+    GROUT_ERR_GROUP = -7,         /* decode group outside [1, 16] */
+    GROUT_ERR_SPLITS = -8,        /* num_splits or block_n out of range */
+    GROUT_ERR_ARG = -9,           /* any other invalid scalar argument */
+    GROUT_ERR_GRAPH = -10         /* graph handle misuse */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* grout_status_string(int32_t status);
+
+/* Limits of the decode kernels. */
+#define GROUT_HEAD_DIM 128
+#define GROUT_MAX_DECODE_GROUP 16
+#define GROUT_MAX_DECODE_SPLITS 1024
+
+/* --------------------------------------------------------- RoPE table (A1) */
+/* Replaces build_inv_freq (src/model.rs:5992-6003): host-side, f32,
+ * out[j] = 1 / theta^((2j)/head_dim) for j < head_dim/2.  No device work. */
+int32_t grout_build_inv_freq(float theta, int32_t head_dim, float* out_host);
+
+/* ---------------------------------------- fused QK norm + RoPE + KV (A2) */
+/* Replaces qk_norm_rope_kv_prefill_raw_f16 (src/kernels.rs:3415-3732) as
+ * launched by execute_qk_norm_rope_kv_prefill_op_ctx (src/model.rs:4463-4598).
+ *   q [seq_len, num_q_heads, 128], k/v [seq_len, num_kv_heads, 128] f16;
+ *   q_weight/k_weight [128] f16; inv_freq [64] f32;
+ *   q_out [seq_len, num_q_heads, 128] f16 (may not alias q);
+ *   k_cache/v_cache [num_kv_heads, max_seq_len, 128] f16, rows
+ *   [position_start, position_start+seq_len) written.
+ * Per row: n = x * rsqrt(sum(x^2)/128 + eps) * w (f32); RoPE on halves
+ * (j, j+64) at theta = f32(position_start+s) * inv_freq[j]; f16 RNE store.
+ * V is copied bit-exactly. */
+int32_t grout_qk_norm_rope_kv_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                      const uint16_t* q_weight, const uint16_t* k_weight,
+                                      const float* inv_freq, uint16_t* q_out,
+                                      uint16_t* k_cache, uint16_t* v_cache, float eps,
+                                      int32_t position_start, int32_t seq_len,
+                                      int32_t num_q_heads, int32_t num_kv_heads,
+                                      int32_t head_dim, int32_t max_seq_len,
+                                      grout_stream_t stream);
+
+/* ---------------------------------------- fused decode variant (A3) */
+/* Replaces qk_norm_rope_kv_decode_raw_f16 (src/kernels.rs:3750-4016) as
+ * recorded in the decode graph (src/model.rs:3194-3221).
+ *   qkv = the QKV GEMV output [Q(num_q_heads*128) | K(num_kv_heads*128) |
+ *   V(num_kv_heads*128)] f16; q_out rows [0, num_q_heads) of a
+ *   [num_q_heads+num_kv_heads, 128] buffer are written;
+ *   *d_position (device u32) is the cache slot and the RoPE position.
+ * A device position >= max_seq_len writes no cache slot (bounds guard). */
+int32_t grout_qk_norm_rope_kv_decode(const uint16_t* qkv, const uint16_t* q_weight,
+                                     const uint16_t* k_weight, const float* inv_freq,
+                                     uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                     const uint32_t* d_position, float eps,
+                                     int32_t num_q_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, int32_t max_seq_len,
+                                     grout_stream_t stream);
+
+/* ------------------------------------------ causal prefill attention (A4-A7) */
+/* Replaces fmha_prefill_causal / fmha_prefill_gqa / fmha_prefill_gqa_lpt /
+ * flash_attn_causal_seq_f16 (src/kernels.rs:1037-1862) as dispatched by
+ * attend_seq_arc_into_ctx_with_position (src/model.rs:5638-5834).
+ *   q [q_len, num_q_heads, 128] f16; K/V read from the caches
+ *   [num_kv_heads, max_seq_len, 128] rows [0, kv_len) with row stride 128 and
+ *   head stride max_seq_len*128 (the explicit cache stride avoids the
+ *   kv_len*D head-stride assumption of src/kernels.rs:1559-1568);
+ *   out [q_len, num_q_heads, 128] f16.
+ * Query row m sits at position query_start+m and attends keys
+ * n < min(kv_len, query_start+m+1); kv_head = q_head / (num_q_heads/num_kv_heads).
+ * Softmax in base 2 with qk_scale/ln2 folded in, f32 accumulation, P rounded
+ * to f16 for the PV product, out = f16(acc / max(l, 1e-8)). */
+int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           uint16_t* out, float qk_scale, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t q_len,
+                           int32_t kv_len, int32_t query_start, int32_t max_seq_len,
+                           grout_stream_t stream);
+
+/* ------------------------------------------------ split-K GQA decode (A9) */
+/* Replaces fmha_decode_gqa_split (src/kernels.rs:2586-2749) as recorded at
+ * src/model.rs:3428-3452.
+ *   q [num_kv_heads, group, 128] f16 (first num_q_heads*128 of q_out);
+ *   s_kv = *d_position + 1 keys are read from the caches;
+ *   att_partial [num_kv_heads, num_splits*group, 128] f16, split-major
+ *   (row split*group + g); lse_partial [num_kv_heads, num_splits*group] f32,
+ *   log2 units.  Split s covers KV tiles of block_n tokens
+ *   [s*per, min(s*per+per, tiles)), tiles = ceil(s_kv/block_n),
+ *   per = ceil(tiles/num_splits) (src/kernels.rs:2624-2629); an empty split
+ *   writes O = 0, LSE = -1e30.
+ *   qk_scale_f16 is the binary16 bit pattern of the scale: grout rounds
+ *   1/sqrt(128) to f16 before the launch (src/model.rs:3427).
+ * A device position >= max_seq_len is clamped to max_seq_len-1 (no reads
+ * outside the cache). */
+int32_t grout_attn_decode_split(const uint16_t* q, const uint16_t* k_cache,
+                                const uint16_t* v_cache, uint16_t* att_partial,
+                                float* lse_partial, uint16_t qk_scale_f16,
+                                const uint32_t* d_position, int32_t num_kv_heads,
+                                int32_t group, int32_t head_dim, int32_t max_seq_len,
+                                int32_t block_n, int32_t num_splits, grout_stream_t stream);
+
+/* ------------------------------------------------------ split-K merge (A10) */
+/* Replaces splitk_reduce_merge (src/kernels.rs:2771-2868) as recorded at
+ * src/model.rs:3453-3473:  w_s = 2^(lse_s - max) / max(sum 2^(lse_s - max), 1e-8),
+ * out[kvh, g, :] = f16(sum_s w_s * att_partial[kvh, s*group+g, :]). */
+int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_partial,
+                                uint16_t* out, int32_t num_kv_heads, int32_t group,
+                                int32_t head_dim, int32_t num_splits, grout_stream_t stream);
+
+/* Bytes of att_partial (f16) and lse_partial (f32) for a split count, as
+ * allocated at src/model.rs:2508-2525.  Returns < 0 on invalid arguments. */
+int64_t grout_attn_decode_partial_bytes(int32_t num_kv_heads, int32_t group, int32_t head_dim,
+                                        int32_t num_splits);
+int64_t grout_attn_decode_lse_bytes(int32_t num_kv_heads, int32_t group, int32_t num_splits);
+
+/* Split count for a decode graph: enough (kv_head, split) workgroups to keep
+ * every CU streaming at the longest context the graph will see, without
+ * splits shorter than a few tiles.  Replaces the fixed NUM_KV_SPLITS default
+ * (src/model.rs:128-135).  Returns >= 1. */
+int32_t grout_attn_decode_pick_splits(int32_t cu_count, int32_t num_kv_heads,
+                                      int32_t max_context, int32_t block_n);
+
+/* Number of compute units of a device (hipDeviceAttributeMultiprocessorCount). */
+int32_t grout_device_cu_count(int32_t device, int32_t* cu_count);
+
+/* --------------------------------------------------- hipGraph helpers (A14) */
+/* Replace cuda-async's CudaGraph::scope / launch (src/model.rs:3118-3648,
+ * :388-391).  begin/end wrap hipStreamBeginCapture / EndCapture +
+ * hipGraphInstantiate on `stream` (thread-local capture mode). */
+typedef struct grout_graph grout_graph;
+int32_t grout_graph_begin(grout_stream_t stream);
+int32_t grout_graph_end(grout_stream_t stream, grout_graph** graph);
+int32_t grout_graph_launch(grout_graph* graph, grout_stream_t stream);
+int32_t grout_graph_destroy(grout_graph* graph);
+
+/* Stream-ordered write of a device u32 (the decode position), replacing the
+ * 4-byte memcpy_htod_async of DecodeCudaGraphRunner::launch_step
+ * (src/model.rs:363-376).  The value travels as a kernel argument, so no host
+ * buffer has to outlive the call. */
+int32_t grout_set_position_async(uint32_t* d_position, uint32_t position,
+                                 grout_stream_t stream);
+
+/* ------------------------------------------- decode graph runner (A14) */
+/* The attention slice of DecodeCudaGraphRunner (src/model.rs:318-493): one
+ * hipGraph holding {fused QK norm/RoPE/KV write, split-K decode, merge} for
+ * one layer's buffers, replayed per token with only the device position
+ * updated.  All pointers are borrowed and must outlive the runner. */
+typedef struct grout_decode_layer {
+    const uint16_t* qkv;       /* [(Hq + 2*Hkv) * 128] f16 QKV GEMV output */
+    const uint16_t* q_weight;  /* [128] f16 */
+    const uint16_t* k_weight;  /* [128] f16 */
+    const float* inv_freq;     /* [64] f32 */
+    uint16_t* q_out;           /* [(Hq + Hkv) * 128] f16 (rows [0,Hq) used) */
+    uint16_t* k_cache;         /* [Hkv, max_seq_len, 128] f16 */
+    uint16_t* v_cache;         /* [Hkv, max_seq_len, 128] f16 */
+    uint16_t* att_partial;     /* grout_attn_decode_partial_bytes */
+    float* lse_partial;        /* grout_attn_decode_lse_bytes */
+    uint16_t* attn_out;        /* [Hkv, G, 128] f16 */
+    uint32_t* d_position;      /* device u32 */
+    float eps;
+    uint16_t qk_scale_f16;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t max_seq_len;
+    int32_t block_n;
+    int32_t num_splits;
+} grout_decode_layer;
+
+typedef struct grout_decode_runner grout_decode_runner;
+/* Validates, runs the three ops once eagerly (the prime pass of
+ * src/model.rs:2561-3115) at `prime_position`, then captures them. */
+int32_t grout_decode_runner_create(const grout_decode_layer* layer, uint32_t prime_position,
+                                   grout_stream_t stream, grout_decode_runner** runner);
+/* launch_step: write the position (stream-ordered), replay the graph.  No host sync. */
+int32_t grout_decode_runner_step(grout_decode_runner* runner, uint32_t position);
+/* zero_kv_caches (src/model.rs:433-462): clear both caches in place; pointers
+ * stay valid for the captured graph.  Synchronises the runner's stream. */
+int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner);
+int32_t grout_decode_runner_destroy(grout_decode_runner* runner);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GROUT_ATTN_HIP_H */

@@ -1,0 +1,165 @@
+"""ctypes wrapper of the CPU oracle (oracle/grout_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` as the checker / CPU baseline; the
+product (``grout_amd``) never imports it.
+
+Arrays are numpy: f16 tensors travel as ``np.float16`` (bit patterns are passed
+to C as uint16), f32 as ``np.float32``.  Every function restates a reference
+function; the C file cites the reference file:line for each.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32 = ctypes.c_int32
+
+
+def build(force: bool = False) -> str:
+    """Compile oracle/liboracle.so with the committed Makefile."""
+    if force or not os.path.exists(_LIB_PATH):
+        cmd = ["make", "-s", "-C", _HERE] + (["-B"] if force else [])
+        subprocess.run(cmd, check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.go_f32_to_f16.restype = ctypes.c_uint16
+        L.go_f32_to_f16.argtypes = [ctypes.c_float]
+        L.go_f16_to_f32.restype = ctypes.c_float
+        L.go_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.go_f32_to_f16_array.argtypes = [_f32p, _u16p, ctypes.c_int64]
+        L.go_f16_to_f32_array.argtypes = [_u16p, _f32p, ctypes.c_int64]
+        L.go_build_inv_freq.argtypes = [ctypes.c_float, _i32, _f32p]
+        L.go_qk_norm_rope_kv_prefill.argtypes = (
+            [_u16p] * 5 + [_f32p] + [_u16p] * 3 + [ctypes.c_float] + [_i32] * 6)
+        L.go_qk_norm_rope_kv_decode.argtypes = (
+            [_u16p] * 3 + [_f32p] + [_u16p] * 3 + [ctypes.c_uint32, ctypes.c_float]
+            + [_i32] * 4)
+        L.go_attn_prefill_f32.argtypes = (
+            [_u16p] * 3 + [_f32p, ctypes.c_float] + [_i32] * 10)
+        L.go_attn_decode_split.argtypes = (
+            [_u16p] * 4 + [_f32p, ctypes.c_uint16, ctypes.c_uint32] + [_i32] * 7)
+        L.go_attn_decode_merge.argtypes = [_u16p, _f32p, _u16p] + [_i32] * 4
+        L.go_decode_split_range.argtypes = [_i32] * 4 + [ctypes.POINTER(_i32)] * 2
+        _lib = L
+    return _lib
+
+
+def _u16(a: np.ndarray):
+    assert a.dtype == np.float16 and a.flags.c_contiguous, (a.dtype, a.flags)
+    return a.ctypes.data_as(_u16p)
+
+
+def _f32(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous, (a.dtype, a.flags)
+    return a.ctypes.data_as(_f32p)
+
+
+# ------------------------------------------------------------------ f16 ----
+
+def f32_to_f16(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.float16)
+    lib().go_f32_to_f16_array(_f32(x), _u16(out), x.size)
+    return out
+
+
+def f16_to_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    out = np.empty(x.shape, dtype=np.float32)
+    lib().go_f16_to_f32_array(_u16(x), _f32(out), x.size)
+    return out
+
+
+def f16_bits(x: float) -> int:
+    """f16 bit pattern of f32(x), as src/model.rs:3427 f16::from_f32(qk_scale)."""
+    return int(lib().go_f32_to_f16(float(np.float32(x))))
+
+
+# ---------------------------------------------------------------- kernels --
+
+def build_inv_freq(theta: float, head_dim: int = 128) -> np.ndarray:
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    lib().go_build_inv_freq(float(np.float32(theta)), head_dim, _f32(out))
+    return out
+
+
+def qk_norm_rope_kv_prefill(q, k, v, q_weight, k_weight, inv_freq, k_cache, v_cache,
+                            eps: float, position_start: int):
+    """Returns q_out; writes k_cache / v_cache in place (like the kernel)."""
+    S, Hq, D = q.shape
+    Hkv = k.shape[1]
+    max_seq = k_cache.shape[1]
+    q_out = np.zeros_like(q)
+    lib().go_qk_norm_rope_kv_prefill(
+        _u16(q), _u16(k), _u16(v), _u16(q_weight), _u16(k_weight), _f32(inv_freq),
+        _u16(q_out), _u16(k_cache), _u16(v_cache), float(eps), position_start, S, Hq, Hkv,
+        D, max_seq)
+    return q_out
+
+
+def qk_norm_rope_kv_decode(qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache,
+                           position: int, eps: float, num_q_heads: int, num_kv_heads: int):
+    D = q_weight.shape[0]
+    max_seq = k_cache.shape[1]
+    lib().go_qk_norm_rope_kv_decode(
+        _u16(qkv), _u16(q_weight), _u16(k_weight), _f32(inv_freq), _u16(q_out),
+        _u16(k_cache), _u16(v_cache), position, float(eps), num_q_heads, num_kv_heads, D,
+        max_seq)
+
+
+def attn_prefill_f32(q, k_cache, v_cache, qk_scale: float, kv_len: int, query_start: int,
+                     row_begin: int = 0, row_step: int = 1, nthreads: int = 0,
+                     out: np.ndarray | None = None) -> np.ndarray:
+    S, Hq, D = q.shape
+    Hkv, max_seq, _ = k_cache.shape
+    if out is None:
+        out = np.zeros((S, Hq, D), dtype=np.float32)
+    lib().go_attn_prefill_f32(
+        _u16(q), _u16(k_cache), _u16(v_cache), _f32(out), float(qk_scale), Hq, Hkv, D, S,
+        kv_len, query_start, max_seq, row_begin, row_step, nthreads)
+    return out
+
+
+def attn_decode_split(q, k_cache, v_cache, qk_scale_f16_bits: int, position: int,
+                      block_n: int, num_splits: int, nthreads: int = 0):
+    """q [Hkv, G, D] f16 -> (att_partial [Hkv, NKS*G, D] f16, lse [Hkv, NKS*G] f32)."""
+    Hkv, G, D = q.shape
+    max_seq = k_cache.shape[1]
+    att = np.zeros((Hkv, num_splits * G, D), dtype=np.float16)
+    lse = np.zeros((Hkv, num_splits * G), dtype=np.float32)
+    lib().go_attn_decode_split(
+        _u16(q), _u16(k_cache), _u16(v_cache), _u16(att), _f32(lse), qk_scale_f16_bits,
+        position, Hkv, G, D, max_seq, block_n, num_splits, nthreads)
+    return att, lse
+
+
+def attn_decode_merge(att, lse, group: int) -> np.ndarray:
+    Hkv, nsg, D = att.shape
+    ns = nsg // group
+    out = np.zeros((Hkv, group, D), dtype=np.float16)
+    lib().go_attn_decode_merge(_u16(att), _f32(lse), _u16(out), Hkv, group, D, ns)
+    return out
+
+
+def decode_split_range(s_kv: int, block_n: int, num_splits: int, split: int):
+    b, e = _i32(), _i32()
+    lib().go_decode_split_range(s_kv, block_n, num_splits, split, ctypes.byref(b),
+                                ctypes.byref(e))
+    return b.value, e.value

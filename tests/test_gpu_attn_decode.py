@@ -1,0 +1,182 @@
+"""GPU parity of split-K GQA decode + merge against the oracle restatement of
+src/kernels.rs:2586-2868 and against the fp32 attention oracle."""
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import (D, assert_close_attn, f16_bits_to_f32, normal_f16,
+                         qk_scale_f16_bits, rng)
+
+pytestmark = pytest.mark.gpu
+
+BN = 32
+
+
+def _decode_gpu(torch, qg, kc, vc, pos, ns, bn=BN):
+    import grout_amd
+
+    hkv, G, _ = qg.shape
+    dq = torch.from_numpy(qg).cuda()
+    dk = torch.from_numpy(kc).cuda()
+    dv = torch.from_numpy(vc).cuda()
+    att, lse = grout_amd.decode_scratch(hkv, G, ns)
+    dpos = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    grout_amd.fmha_decode_gqa_split(dq, dk, dv, att, lse, qk_scale_f16_bits(), dpos, bn)
+    out = torch.empty((hkv, G, D), dtype=torch.float16, device="cuda")
+    grout_amd.splitk_reduce_merge(att, lse, out)
+    torch.cuda.synchronize()
+    return att.cpu().numpy(), lse.cpu().numpy(), out.cpu().numpy()
+
+
+def _case(seed, hq, hkv, MS):
+    g = rng(seed)
+    qg = normal_f16(g, (hkv, hq // hkv, D))
+    kc = normal_f16(g, (hkv, MS, D))
+    vc = normal_f16(g, (hkv, MS, D))
+    return qg, kc, vc
+
+
+def _fp32_decode(qg, kc, vc, pos):
+    hkv, G, _ = qg.shape
+    q = np.ascontiguousarray(qg.reshape(1, hkv * G, D))
+    scale = f16_bits_to_f32(qk_scale_f16_bits())
+    out = oracle.attn_prefill_f32(q, kc, vc, scale, kv_len=pos + 1, query_start=pos)
+    return out.reshape(hkv, G, D)
+
+
+@pytest.mark.parametrize("hq,hkv,pos,MS,ns,seed", [
+    (32, 8, 4096, 4200, 16, 1),    # config c2 with the reference's NKS=16
+    (32, 8, 4096, 4200, 43, 2),    # c2, split count that does not divide the tiles
+    (64, 8, 2047, 2048, 64, 3),    # G = 8, cache full to the last slot
+    (4, 2, 0, 8, 4, 4),            # s_kv = 1: three empty splits
+    (16, 8, 100, 128, 1, 5),       # one split
+    (8, 8, 777, 800, 8, 6),        # MHA decode (G = 1)
+    (48, 4, 300, 320, 5, 7),       # G = 12
+])
+def test_split_and_merge_match_oracle(gpu, hq, hkv, pos, MS, ns, seed):
+    import torch
+
+    qg, kc, vc = _case(seed, hq, hkv, MS)
+    att, lse, out = _decode_gpu(torch, qg, kc, vc, pos, ns)
+    att_ref, lse_ref = oracle.attn_decode_split(qg, kc, vc, qk_scale_f16_bits(), pos, BN, ns)
+    out_ref = oracle.attn_decode_merge(att_ref, lse_ref, qg.shape[1])
+
+    s_kv = pos + 1
+    nonempty = np.array([oracle.decode_split_range(s_kv, BN, ns, s)[0]
+                         < oracle.decode_split_range(s_kv, BN, ns, s)[1] for s in range(ns)])
+    G = qg.shape[1]
+    rows = np.repeat(nonempty, G)
+    # Empty splits carry exactly O = 0, LSE = -1e30 (weight 0 in the merge).
+    assert np.all(att[:, ~rows] == 0)
+    assert np.all(lse[:, ~rows] == np.float32(-1e30))
+    assert_close_attn(att[:, rows], att_ref[:, rows], "att_partial")
+    assert np.max(np.abs(lse[:, rows] - lse_ref[:, rows])) < 1e-3
+    assert_close_attn(out, out_ref, "merged vs oracle merge")
+    assert_close_attn(out, _fp32_decode(qg, kc, vc, pos), "merged vs fp32 decode")
+
+
+def test_split_invariance(gpu):
+    """NKS = 1 and NKS = k give the same attention up to f16 partial rounding."""
+    import torch
+
+    qg, kc, vc = _case(50, 32, 8, 3000)
+    _, _, o1 = _decode_gpu(torch, qg, kc, vc, 2999, 1)
+    _, _, o7 = _decode_gpu(torch, qg, kc, vc, 2999, 7)
+    _, _, o64 = _decode_gpu(torch, qg, kc, vc, 2999, 64)
+    assert_close_attn(o7, o1, "NKS=7 vs 1")
+    assert_close_attn(o64, o1, "NKS=64 vs 1")
+
+
+def test_single_key_returns_v0(gpu):
+    import torch
+
+    qg, kc, vc = _case(51, 16, 4, 64)
+    _, _, out = _decode_gpu(torch, qg, kc, vc, 0, 3)
+    for h in range(4):
+        for gg in range(4):
+            assert np.array_equal(out[h, gg].view(np.uint16), vc[h, 0].view(np.uint16))
+
+
+def test_position_clamped_to_cache(gpu):
+    """A device position beyond the cache reads no memory outside it: it behaves
+    as position max_seq_len-1."""
+    import torch
+
+    qg, kc, vc = _case(52, 32, 8, 256)
+    _, _, a = _decode_gpu(torch, qg, kc, vc, 255, 8)
+    _, _, b = _decode_gpu(torch, qg, kc, vc, 100000, 8)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
+def test_decode_equals_prefill_last_row(gpu):
+    """A decode at position p equals row p of a causal prefill (same f16-rounded scale)."""
+    import torch
+
+    import grout_amd
+
+    hq, hkv, MS, pos = 32, 8, 1100, 1024
+    qg, kc, vc = _case(53, hq, hkv, MS)
+    _, _, out = _decode_gpu(torch, qg, kc, vc, pos, 16)
+    q = torch.from_numpy(np.ascontiguousarray(qg.reshape(1, hq, D))).cuda()
+    o2 = torch.empty_like(q)
+    grout_amd.attend_prefill(q, torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda(), o2,
+                             pos, qk_scale=f16_bits_to_f32(qk_scale_f16_bits()))
+    torch.cuda.synchronize()
+    assert_close_attn(out.reshape(1, hq, D), o2.cpu().numpy().astype(np.float32),
+                      "decode vs prefill row")
+
+
+def test_graph_runner_replay(gpu):
+    """DecodeGraphRunner: capture once, replay at successive positions; each replay
+    equals the eager ops and the oracle (norm/RoPE/KV write + split + merge)."""
+    import torch
+
+    import grout_amd
+    from tests._util import EPS, THETA, norm_weight
+
+    g = rng(60)
+    hq, hkv, MS, p0 = 32, 8, 640, 500
+    G = hq // hkv
+    kc = normal_f16(g, (hkv, MS, D))
+    vc = normal_f16(g, (hkv, MS, D))
+    qw, kw = norm_weight(g), norm_weight(g)
+    inv = oracle.build_inv_freq(THETA)
+    ns = 12
+    dev = dict(
+        qkv=torch.zeros(((hq + 2 * hkv) * D,), dtype=torch.float16, device="cuda"),
+        q_weight=torch.from_numpy(qw).cuda(), k_weight=torch.from_numpy(kw).cuda(),
+        inv_freq=torch.from_numpy(inv).cuda(),
+        q_out=torch.zeros(((hq + hkv), D), dtype=torch.float16, device="cuda"),
+        k_cache=torch.from_numpy(kc).cuda(), v_cache=torch.from_numpy(vc).cuda(),
+        attn_out=torch.zeros((hkv, G, D), dtype=torch.float16, device="cuda"),
+        position=torch.zeros((1,), dtype=torch.int32, device="cuda"),
+    )
+    att, lse = grout_amd.decode_scratch(hkv, G, ns)
+    runner = grout_amd.DecodeGraphRunner(
+        **dev, att_partial=att, lse_partial=lse, eps=EPS, qk_scale_f16_bits=qk_scale_f16_bits(),
+        num_q_heads=hq, num_kv_heads=hkv, num_splits=ns, prime_position=p0)
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    try:
+        for step in range(5):
+            pos = p0 + step
+            qkv = normal_f16(g, ((hq + 2 * hkv) * D,))
+            with torch.cuda.stream(runner.stream):
+                dev["qkv"].copy_(torch.from_numpy(qkv).cuda())
+                runner.launch_step(pos)
+            runner.stream.synchronize()
+            out = dev["attn_out"].cpu().numpy()
+            qo_ref = np.zeros(((hq + hkv), D), dtype=np.float16)
+            oracle.qk_norm_rope_kv_decode(qkv, qw, kw, inv, qo_ref, kc_ref, vc_ref, pos, EPS,
+                                          hq, hkv)
+            qg = np.ascontiguousarray(qo_ref[:hq].reshape(hkv, G, D))
+            a_ref, l_ref = oracle.attn_decode_split(qg, kc_ref, vc_ref, qk_scale_f16_bits(),
+                                                    pos, BN, ns)
+            assert_close_attn(out, oracle.attn_decode_merge(a_ref, l_ref, G), f"replay {step}")
+        # The prime pass wrote slot p0 once before capture; the replays rewrote it.
+        kc_dev = dev["k_cache"].cpu().numpy()
+        from tests._util import f16_ulp_diff
+        assert f16_ulp_diff(kc_dev, kc_ref).max() <= 1
+        runner.zero_kv_caches()
+        assert int(dev["k_cache"].abs().sum().item()) == 0
+    finally:
+        runner.close()

@@ -1,0 +1,115 @@
+"""GPU parity of the causal flash-attention prefill against the fp32 oracle.
+
+Contract: |gpu - oracle| <= 2e-3 + 1e-2*|oracle| elementwise, oracle =
+benchmarks/src/bin/attention_microbench.rs:665-702 generalised to GQA on the cache.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import D, assert_close_attn, normal_f16, rng
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 1.0 / math.sqrt(D)
+
+
+def _run(torch, q, kc, vc, qs, kv_len=None):
+    import grout_amd
+
+    dq = torch.from_numpy(q).cuda()
+    dk = torch.from_numpy(kc).cuda()
+    dv = torch.from_numpy(vc).cuda()
+    out = torch.empty_like(dq)
+    grout_amd.attend_prefill(dq, dk, dv, out, qs, kv_len=kv_len)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _case(seed, hq, hkv, S, qs, MS, scale_rows=None):
+    g = rng(seed)
+    q = normal_f16(g, (S, hq, D))
+    kc = normal_f16(g, (hkv, MS, D))
+    vc = normal_f16(g, (hkv, MS, D))
+    if scale_rows is not None:
+        idx = g.random((hkv, MS)) < scale_rows
+        kc[idx] = (kc[idx].astype(np.float32) * 8).astype(np.float16)
+    return q, kc, vc
+
+
+@pytest.mark.parametrize("hq,hkv,S,qs,MS,seed", [
+    (16, 8, 512, 0, 512, 1),      # config c1
+    (4, 2, 17, 0, 17, 2),         # tiny, ragged
+    (4, 2, 64, 5, 80, 3),         # query_start > 0 on a padded cache
+    (8, 8, 100, 0, 128, 4),       # MHA (G = 1), ragged
+    (64, 8, 130, 0, 160, 5),      # G = 8 (Qwen3-32B heads)
+    (32, 8, 1, 0, 1, 6),          # single row
+    (32, 8, 257, 1000, 1400, 7),  # chunked suffix far into the cache
+    (12, 4, 200, 0, 200, 8),      # G = 3 (workgroups straddle position tiles)
+])
+def test_prefill_matches_oracle(gpu, hq, hkv, S, qs, MS, seed):
+    import torch
+
+    q, kc, vc = _case(seed, hq, hkv, S, qs, MS)
+    out = _run(torch, q, kc, vc, qs)
+    ref = oracle.attn_prefill_f32(q, kc, vc, SCALE, kv_len=qs + S, query_start=qs)
+    assert_close_attn(out, ref, f"prefill hq={hq} hkv={hkv} S={S} qs={qs}")
+
+
+def test_prefill_first_row_is_v0(gpu):
+    """Row 0 at position 0 sees only key 0: p = 1, l = 1, out = V[kvh, 0] exactly."""
+    import torch
+
+    q, kc, vc = _case(40, 8, 2, 96, 0, 96)
+    out = _run(torch, q, kc, vc, 0)
+    for h in range(8):
+        assert np.array_equal(out[0, h].view(np.uint16), vc[h // 4, 0].view(np.uint16))
+
+
+def test_prefill_outlier_keys(gpu):
+    """1% of K rows scaled x8 (config c5's online-softmax stress), S=1024."""
+    import torch
+
+    q, kc, vc = _case(41, 64, 8, 1024, 0, 1024, scale_rows=0.01)
+    out = _run(torch, q, kc, vc, 0)
+    ref = oracle.attn_prefill_f32(q, kc, vc, SCALE, kv_len=1024, query_start=0)
+    assert_close_attn(out, ref, "prefill outliers")
+
+
+def test_chunked_prefill_equals_full(gpu):
+    """src/model.rs:6134-6205 invariant: a suffix prefill at query_start>0 over the
+    cached prefix equals the same rows of a full prefill."""
+    import torch
+
+    q, kc, vc = _case(42, 32, 8, 384, 0, 384)
+    full = _run(torch, q, kc, vc, 0)
+    cut = 200
+    part = _run(torch, np.ascontiguousarray(q[cut:]), kc, vc, cut)
+    assert_close_attn(part, full[cut:].astype(np.float32), "chunked vs full", atol=1e-3, rtol=0)
+
+
+def test_gqa_equals_mha_with_repeated_kv(gpu):
+    import torch
+
+    hq, hkv, S = 8, 2, 150
+    q, kc, vc = _case(43, hq, hkv, S, 0, S)
+    out = _run(torch, q, kc, vc, 0)
+    kr = np.ascontiguousarray(np.repeat(kc, hq // hkv, axis=0))
+    vr = np.ascontiguousarray(np.repeat(vc, hq // hkv, axis=0))
+    out_mha = _run(torch, q, kr, vr, 0)
+    assert np.array_equal(out.view(np.uint16), out_mha.view(np.uint16))
+
+
+@pytest.mark.parametrize("S", [2048])
+def test_prefill_long_sampled_rows(gpu, S):
+    """Qwen3-4B heads at S=2048; oracle on a stride sample of rows."""
+    import torch
+
+    q, kc, vc = _case(44, 32, 8, S, 0, S)
+    out = _run(torch, q, kc, vc, 0)
+    ref = oracle.attn_prefill_f32(q, kc, vc, SCALE, kv_len=S, query_start=0, row_begin=3,
+                                  row_step=61)
+    rows = np.arange(3, S, 61)
+    assert_close_attn(out[rows], ref[rows], "prefill S=2048 sampled")

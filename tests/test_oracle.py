@@ -1,0 +1,313 @@
+"""Pins the CPU oracle (oracle/grout_oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something that does not restate its
+own formula: the reference's KV-slot known-answer test (tests/kernels.rs:67-118),
+closed forms, invariants, numpy's f16 conversion, an independent float64
+formulation, and torch's CPU scaled_dot_product_attention.  Each check is chosen
+so a plausible slip (dropped term, wrong sign or half pairing, wrong index or
+stride, transposed operand, wrong split boundary) fails at least one of them.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import D, EPS, THETA, f16_ulp_diff, norm_weight, normal_f16, qk_scale_f16_bits, rng
+
+SCALE = 1.0 / math.sqrt(D)
+
+
+# ------------------------------------------------------------------- f16 --
+
+def test_f16_conversion_matches_numpy():
+    g = np.random.default_rng(0)
+    x = np.concatenate([
+        g.standard_normal(200000).astype(np.float32) * np.float32(3000),
+        g.standard_normal(50000).astype(np.float32) * np.float32(1e-5),   # f16 subnormals
+        np.float32([0.0, -0.0, 65504, 65519.99, 65520, -65520, 2.0 ** -24, 2.0 ** -25,
+                    2.0 ** -25 * 1.0001, 3 * 2.0 ** -26, 6.1035156e-05, np.inf, -np.inf]),
+    ])
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16)
+    assert np.array_equal(oracle.f32_to_f16(x).view(np.uint16), ref.view(np.uint16))
+    allbits = np.arange(65536, dtype=np.uint16).view(np.float16)
+    finite = np.isfinite(allbits)
+    back = oracle.f16_to_f32(allbits)
+    assert np.array_equal(back[finite], allbits[finite].astype(np.float32))
+    assert np.all(np.isnan(back[np.isnan(allbits)]))
+
+
+# -------------------------------------------------------------- inv_freq --
+
+def test_inv_freq_closed_form():
+    inv = oracle.build_inv_freq(THETA)
+    assert inv.shape == (64,) and inv[0] == 1.0
+    j = np.arange(64)
+    exact = THETA ** (-(2.0 * j) / D)
+    assert np.allclose(inv, exact, rtol=3e-7, atol=0)
+    assert abs(inv[32] - 1e-3) < 1e-9  # theta^(-1/2)
+    assert np.all(np.diff(inv) < 0)
+    # Qwen3 default theta 1e4 gives the textbook 10000^(-2j/d) table.
+    inv4 = oracle.build_inv_freq(1e4)
+    assert np.allclose(inv4, 1e4 ** (-(2.0 * j) / D), rtol=3e-7)
+
+
+# ------------------------------------------------------- fused norm/RoPE --
+
+def _rope_f64(x, w, inv, pos):
+    """Independent float64 formulation: RMSNorm then rotate each (j, j+64) pair
+    as a complex number by the f32 angle f32(pos)*inv_freq[j]."""
+    x = x.astype(np.float64)
+    n = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + EPS) * w.astype(np.float64)
+    theta = (np.float32(pos) * inv).astype(np.float64)
+    z = (n[..., :64] + 1j * n[..., 64:]) * np.exp(1j * theta)
+    return np.concatenate([z.real, z.imag], axis=-1)
+
+
+def _prefill(q, k, v, qw, kw, ps, MS, fill=0.0):
+    hkv = k.shape[1]
+    kc = np.full((hkv, MS, D), fill, dtype=np.float16)
+    vc = np.full((hkv, MS, D), fill, dtype=np.float16)
+    inv = oracle.build_inv_freq(THETA)
+    qo = oracle.qk_norm_rope_kv_prefill(q, k, v, qw, kw, inv, kc, vc, EPS, ps)
+    return qo, kc, vc
+
+
+def test_kv_slot_known_answer():
+    """Reference KAT tests/kernels.rs:67-118 (HEADS=2, CAPACITY=16, START=3, ROWS=5,
+    values i+1) on the fused op's V path, D=128: every slot exact, zeros elsewhere."""
+    HEADS, CAPACITY, ROWS, START = 2, 16, 5, 3
+    values = (np.arange(ROWS * HEADS * D) + 1).astype(np.float16).reshape(ROWS, HEADS, D)
+    ones = np.ones(D, dtype=np.float16)
+    _, _, vc = _prefill(np.zeros_like(values), values, values, ones, ones, START, CAPACITY)
+    for head in range(HEADS):
+        for pos in range(CAPACITY):
+            exp = values[pos - START, head] if START <= pos < START + ROWS else np.zeros(D)
+            assert np.array_equal(vc[head, pos].astype(np.float32), exp.astype(np.float32))
+
+
+@pytest.mark.parametrize("ps,seed", [(0, 1), (5, 2), (32700, 3)])
+def test_norm_rope_matches_float64(ps, seed):
+    g = rng(seed)
+    S, hq, hkv = 9, 4, 2
+    q, k, v = normal_f16(g, (S, hq, D)), normal_f16(g, (S, hkv, D)), normal_f16(g, (S, hkv, D))
+    qw, kw = norm_weight(g), norm_weight(g)
+    qo, kc, vc = _prefill(q, k, v, qw, kw, ps, ps + S + 3)
+    inv = oracle.build_inv_freq(THETA)
+    pos = ps + np.arange(S)
+    qr = np.stack([_rope_f64(q[s], qw, inv, pos[s]) for s in range(S)])
+    kr = np.stack([_rope_f64(k[s], kw, inv, pos[s]) for s in range(S)])
+    assert f16_ulp_diff(qo, qr.astype(np.float16)).max() <= 1
+    assert f16_ulp_diff(kc[:, ps:ps + S].transpose(1, 0, 2), kr.astype(np.float16)).max() <= 1
+    assert np.array_equal(vc[:, ps:ps + S].transpose(1, 0, 2), v)
+
+
+def test_rope_single_element_pairs_j_with_j_plus_64():
+    """x = a*e_0: n_0 = sqrt(128)*w_0, y_0 = n_0 cos(pos), y_64 = n_0 sin(pos)
+    (inv_freq[0] = 1); every other element stays 0.  Pins the half pairing and
+    the rotation direction."""
+    x = np.zeros((1, 1, D), dtype=np.float16)
+    x[0, 0, 0] = 3.0
+    ones = np.ones(D, dtype=np.float16)
+    pos = 2
+    qo, _, _ = _prefill(x, x[:, :1], x[:, :1], ones, ones, pos, pos + 1)
+    n0 = 3.0 / math.sqrt(9.0 / 128 + EPS)
+    assert qo[0, 0, 0] == np.float16(n0 * math.cos(2.0))
+    assert qo[0, 0, 64] == np.float16(n0 * math.sin(2.0))
+    assert np.count_nonzero(qo) == 2
+
+
+def test_rope_relative_position_invariance():
+    """<rope(q,a), rope(k,b)> depends only on a-b (same rotation for q and k)."""
+    g = rng(4)
+    q = normal_f16(g, (1, 1, D))
+    k = normal_f16(g, (1, 1, D))
+    ones = np.ones(D, dtype=np.float16)
+
+    def dot(a, b):
+        qa, _, _ = _prefill(q, k, k, ones, ones, a, a + 1)
+        _, kb, _ = _prefill(q, k, k, ones, ones, b, b + 1)
+        return float(np.dot(qa[0, 0].astype(np.float64), kb[0, b].astype(np.float64)))
+
+    d1, d2, d3 = dot(10, 3), dot(110, 103), dot(3, 10)
+    assert abs(d1 - d2) < 0.05 and abs(d1 - d3) > 0.05
+
+
+def test_decode_equals_prefill_row():
+    g = rng(5)
+    hq, hkv, MS, pos = 8, 2, 40, 33
+    qkv = normal_f16(g, ((hq + 2 * hkv) * D,))
+    qw, kw = norm_weight(g), norm_weight(g)
+    inv = oracle.build_inv_freq(THETA)
+    qo = np.zeros((hq + hkv, D), dtype=np.float16)
+    kc, vc = np.zeros((hkv, MS, D), np.float16), np.zeros((hkv, MS, D), np.float16)
+    oracle.qk_norm_rope_kv_decode(qkv, qw, kw, inv, qo, kc, vc, pos, EPS, hq, hkv)
+    q = qkv[:hq * D].reshape(1, hq, D)
+    k = qkv[hq * D:(hq + hkv) * D].reshape(1, hkv, D)
+    v = qkv[(hq + hkv) * D:].reshape(1, hkv, D)
+    qo2, kc2, vc2 = _prefill(q, k, v, qw, kw, pos, MS)
+    assert np.array_equal(qo[:hq], qo2[0]) and np.all(qo[hq:] == 0)
+    assert np.array_equal(kc, kc2) and np.array_equal(vc, vc2)
+
+
+# ------------------------------------------------------ prefill attention --
+
+def _attn_f64(q, kc, vc, scale, kv_len, qs):
+    S, hq, _ = q.shape
+    hkv = kc.shape[0]
+    G = hq // hkv
+    out = np.zeros((S, hq, D))
+    for h in range(hq):
+        K = kc[h // G, :kv_len].astype(np.float64)
+        V = vc[h // G, :kv_len].astype(np.float64)
+        s = q[:, h].astype(np.float64) @ K.T * scale
+        pos = qs + np.arange(S)[:, None]
+        s = np.where(np.arange(kv_len)[None, :] <= pos, s, -np.inf)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ V
+    return out
+
+
+@pytest.mark.parametrize("hq,hkv,S,qs,MS", [(4, 2, 17, 0, 17), (4, 2, 9, 5, 20),
+                                            (6, 3, 33, 0, 40), (2, 2, 64, 0, 64)])
+def test_attention_matches_float64_bruteforce(hq, hkv, S, qs, MS):
+    g = rng(6)
+    q, kc, vc = normal_f16(g, (S, hq, D)), normal_f16(g, (hkv, MS, D)), normal_f16(g, (hkv, MS, D))
+    out = oracle.attn_prefill_f32(q, kc, vc, SCALE, qs + S, qs)
+    ref = _attn_f64(q, kc, vc, SCALE, qs + S, qs)
+    assert np.max(np.abs(out - ref)) < 2e-5
+
+
+def test_attention_matches_torch_sdpa():
+    torch = pytest.importorskip("torch")
+    g = rng(7)
+    S, hq, hkv = 48, 8, 2
+    q, kc, vc = normal_f16(g, (S, hq, D)), normal_f16(g, (hkv, S, D)), normal_f16(g, (hkv, S, D))
+    out = oracle.attn_prefill_f32(q, kc, vc, SCALE, S, 0)
+    tq = torch.from_numpy(q.astype(np.float32)).permute(1, 0, 2)
+    tk = torch.from_numpy(kc.astype(np.float32)).repeat_interleave(hq // hkv, dim=0)
+    tv = torch.from_numpy(vc.astype(np.float32)).repeat_interleave(hq // hkv, dim=0)
+    ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=True,
+                                                           scale=SCALE)
+    assert np.max(np.abs(out - ref.permute(1, 0, 2).numpy())) < 2e-5
+
+
+def test_attention_special_cases():
+    g = rng(8)
+    S, hq, hkv = 12, 4, 2
+    q, kc, vc = normal_f16(g, (S, hq, D)), normal_f16(g, (hkv, S, D)), normal_f16(g, (hkv, S, D))
+    out = oracle.attn_prefill_f32(q, kc, vc, SCALE, S, 0)
+    # Row 0 sees only key 0.
+    for h in range(hq):
+        assert np.array_equal(out[0, h], vc[h // 2, 0].astype(np.float32))
+    # Identical keys: uniform weights -> causal prefix mean of V.
+    kc_same = np.repeat(kc[:, :1], S, axis=1)
+    o2 = oracle.attn_prefill_f32(q, kc_same, vc, SCALE, S, 0)
+    for m in range(S):
+        assert np.allclose(o2[m, 0], vc[0, :m + 1].astype(np.float64).mean(0), atol=1e-5)
+    # One dominant key: the row returns that V row.
+    kc_dom = np.zeros_like(kc)
+    qd = np.zeros_like(q)
+    qd[:, :, 0] = 8.0
+    kc_dom[:, 3, 0] = 64.0
+    o3 = oracle.attn_prefill_f32(qd, kc_dom, vc, SCALE, S, 0)
+    assert np.allclose(o3[5:, 0], vc[0, 3].astype(np.float32), atol=1e-6)
+
+
+def test_attention_chunked_equals_full_and_row_sampling():
+    g = rng(9)
+    S, hq, hkv = 40, 4, 2
+    q, kc, vc = normal_f16(g, (S, hq, D)), normal_f16(g, (hkv, S, D)), normal_f16(g, (hkv, S, D))
+    full = oracle.attn_prefill_f32(q, kc, vc, SCALE, S, 0)
+    part = oracle.attn_prefill_f32(np.ascontiguousarray(q[25:]), kc, vc, SCALE, S, 25)
+    assert np.array_equal(full[25:], part)
+    samp = oracle.attn_prefill_f32(q, kc, vc, SCALE, S, 0, row_begin=3, row_step=7)
+    rows = np.arange(3, S, 7)
+    assert np.array_equal(samp[rows], full[rows])
+    others = np.setdiff1d(np.arange(S), rows)
+    assert np.all(samp[others] == 0)
+
+
+# ---------------------------------------------------------- split decode --
+
+def test_split_ranges_partition_tiles():
+    for s_kv in (1, 31, 32, 33, 4097, 32769):
+        for ns in (1, 3, 16, 64, 200):
+            tiles = -(-s_kv // 32)
+            covered = []
+            for s in range(ns):
+                b, e = oracle.decode_split_range(s_kv, 32, ns, s)
+                covered.extend(range(b, max(b, e)))
+            assert covered == list(range(tiles)), (s_kv, ns)
+
+
+def _dec_case(seed, hkv, G, MS):
+    g = rng(seed)
+    return (normal_f16(g, (hkv, G, D)), normal_f16(g, (hkv, MS, D)), normal_f16(g, (hkv, MS, D)))
+
+
+@pytest.mark.parametrize("ns", [1, 5, 16])
+def test_split_merge_matches_float64_decode(ns):
+    qg, kc, vc = _dec_case(10, 2, 4, 300)
+    pos = 260
+    att, lse = oracle.attn_decode_split(qg, kc, vc, qk_scale_f16_bits(), pos, 32, ns)
+    out = oracle.attn_decode_merge(att, lse, 4).astype(np.float32)
+    scale = float(np.array([qk_scale_f16_bits()], np.uint16).view(np.float16)[0])
+    q = qg.reshape(1, 8, D)
+    ref = _attn_f64(q, kc, vc, scale, pos + 1, pos).reshape(2, 4, D)
+    assert np.max(np.abs(out - ref)) < 2e-3
+    # Each non-empty partial is itself the softmax over its token range.
+    s_kv = pos + 1
+    for s in range(ns):
+        b, e = oracle.decode_split_range(s_kv, 32, ns, s)
+        if b >= e:
+            continue
+        lo, hi = b * 32, min(e * 32, s_kv)
+        for h in range(2):
+            K = kc[h, lo:hi].astype(np.float64)
+            logits = qg[h].astype(np.float64) @ K.T * scale
+            p = np.exp(logits - logits.max(1, keepdims=True))
+            part = p / p.sum(1, keepdims=True) @ vc[h, lo:hi].astype(np.float64)
+            rows = slice(s * 4, s * 4 + 4)
+            assert np.max(np.abs(att[h, rows].astype(np.float64) - part)) < 2e-3
+            lse_ref = (np.log(np.exp(logits).sum(1))) / math.log(2)
+            assert np.max(np.abs(lse[h, rows] - lse_ref)) < 1e-4
+
+
+def test_empty_split_and_single_key():
+    qg, kc, vc = _dec_case(11, 2, 4, 64)
+    att, lse = oracle.attn_decode_split(qg, kc, vc, qk_scale_f16_bits(), 0, 32, 4)
+    assert np.all(att[:, 4:] == 0) and np.all(lse[:, 4:] == np.float32(-1e30))
+    out = oracle.attn_decode_merge(att, lse, 4)
+    for h in range(2):
+        assert np.array_equal(out[h], np.repeat(vc[h, :1], 4, axis=0))
+
+
+def test_merge_closed_forms():
+    hkv, G, ns = 1, 2, 2
+    att = np.zeros((hkv, ns * G, D), dtype=np.float16)
+    att[0, 0:2] = 1.0   # split 0
+    att[0, 2:4] = 4.0   # split 1
+    lse = np.zeros((hkv, ns * G), dtype=np.float32)
+    out = oracle.attn_decode_merge(att, lse, G)
+    assert np.all(out == np.float16(2.5))  # equal LSE -> mean
+    lse[0, 2:4] = 1.0  # split 1 twice as heavy (log2 units)
+    out = oracle.attn_decode_merge(att, lse, G)
+    assert np.allclose(out.astype(np.float32), (1.0 + 2 * 4.0) / 3, atol=2e-3)
+
+
+def test_split_invariance_oracle():
+    qg, kc, vc = _dec_case(12, 2, 8, 1000)
+    outs = []
+    for ns in (1, 4, 31):
+        att, lse = oracle.attn_decode_split(qg, kc, vc, qk_scale_f16_bits(), 999, 32, ns)
+        outs.append(oracle.attn_decode_merge(att, lse, 8).astype(np.float32))
+    assert np.max(np.abs(outs[1] - outs[0])) < 2e-3
+    assert np.max(np.abs(outs[2] - outs[0])) < 2e-3
+
+
+def test_decode_scale_is_f16_rounded():
+    """src/model.rs:3427: the decode scale is f16(1/sqrt(128)) = 0.08837890625."""
+    assert qk_scale_f16_bits() == 0x2DA8 == oracle.f16_bits(SCALE)
+    assert float(np.array([0x2DA8], np.uint16).view(np.float16)[0]) == 0.08837890625
