@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen3 attention hot path on one MI355X.
+
+Headline (BASELINE.json metric): prefill attention TFLOP/s as a fraction of the
+fp16 dense MFMA peak, and decode attention GB/s as a fraction of HBM peak.
+
+  value   = config c3: Qwen3-4B causal prefill attention, batch 1, S=8192,
+            32 Q / 8 KV heads, head_dim 128, f16 in / f32 accumulate.
+            One step = one grout_attn_prefill launch; inputs already in HBM.
+  decode  = config c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context
+            32768, {fused norm/RoPE/KV write, split-K decode, merge} captured
+            in a hipGraph and replayed 1000x with only the position updated.
+  also    = c3's fused QK norm/RoPE/KV write (HBM-bound) and c2 (Qwen3-4B
+            decode at context 4096).
+
+Kernel durations come from HIP events recorded on the launch stream around
+each launch.  The CPU baseline is the oracle (a C port of the reference's fp32
+CPU attention, benchmarks/src/bin/attention_microbench.rs:665-702) run on a
+bounded row sample of the same inputs.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = ("prefill attn TFLOP/s (% fp16 MFMA peak); decode attn GB/s (% HBM peak), 1 GPU")
+PEAK_TFLOPS_F16 = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz (dense fp16 MFMA)
+PEAK_HBM_GBS = 8000.0      # HBM3E
+D = 128
+EPS = 1e-6
+THETA = 1e6
+
+
+def prefill_flops(hq: int, q_len: int, query_start: int = 0) -> float:
+    """2*D*Hq*sum_{m<S}(ps+m+1) x 2 (QK^T and PV MACs, causal incl. diagonal)."""
+    pairs = q_len * query_start + q_len * (q_len + 1) // 2
+    return 2.0 * 2.0 * D * hq * pairs
+
+
+def decode_bytes(hq: int, hkv: int, s_kv: int) -> int:
+    """K+V read for s_kv keys plus Q in and O out (split scratch not counted)."""
+    return 2 * hkv * s_kv * D * 2 + 2 * hq * D * 2
+
+
+def norm_bytes(hq: int, hkv: int, S: int) -> int:
+    """q,k,v read + q_out, k_cache, v_cache rows written."""
+    return 2 * S * D * 2 * (hq + 2 * hkv)
+
+
+def _events(torch, n):
+    return [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(n)]
+
+
+def time_launches(torch, fn, steps: int, warmup: int, stream=None):
+    """Per-launch durations (ms) from event pairs on the launch stream, plus the
+    wall time of the whole timed region (ms) between two synchronizations."""
+    s = stream or torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = _events(torch, steps)
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record(s)
+        fn()
+        b.record(s)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    durs = [a.elapsed_time(b) for a, b in evs]
+    return durs, wall
+
+
+def bench_prefill(torch, ga, steps, warmup, gen):
+    hq, hkv, S = 32, 8, 8192
+    q = torch.randn((S, hq, D), device="cuda", generator=gen, dtype=torch.float32).half()
+    kc = torch.randn((hkv, S, D), device="cuda", generator=gen, dtype=torch.float32).half()
+    vc = torch.randn((hkv, S, D), device="cuda", generator=gen, dtype=torch.float32).half()
+    out = torch.empty_like(q)
+    fn = lambda: ga.attend_prefill(q, kc, vc, out, 0)  # noqa: E731
+    durs, wall = time_launches(torch, fn, steps, warmup)
+    assert torch.isfinite(out).all().item(), "non-finite prefill output"
+    ms = sum(durs) / len(durs)
+    flops = prefill_flops(hq, S)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return dict(q=q, kc=kc, vc=vc, out=out, ms=ms, wall_ms=wall, tflops=tflops, flops=flops,
+                hq=hq, hkv=hkv, S=S)
+
+
+def bench_norm(torch, ga, steps, warmup, gen):
+    hq, hkv, S = 32, 8, 8192
+    q = torch.randn((S, hq, D), device="cuda", generator=gen).half()
+    k = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
+    v = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
+    qw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    kw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    inv = ga.build_inv_freq(THETA).cuda()
+    kc = torch.zeros((hkv, S, D), device="cuda", dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    out = torch.empty_like(q)
+    fn = lambda: ga.qk_norm_rope_kv_prefill(q, k, v, qw, kw, inv, out, kc, vc, EPS, 0)  # noqa
+    durs, _ = time_launches(torch, fn, steps, warmup)
+    ms = sum(durs) / len(durs)
+    nb = norm_bytes(hq, hkv, S)
+    return dict(ms=ms, bytes=nb, gbs=nb / (ms * 1e-3) / 1e9)
+
+
+def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
+    """Graph replay of {norm/RoPE/KV write, split, merge} at positions ctx..ctx+replays-1,
+    plus event-timed eager launches of the split kernel alone at position ctx."""
+    G = hq // hkv
+    MS = ctx + max(replays, 1024)
+    kc = torch.randn((hkv, MS, D), device="cuda", generator=gen).half()
+    vc = torch.randn((hkv, MS, D), device="cuda", generator=gen).half()
+    qkv = torch.randn(((hq + 2 * hkv) * D,), device="cuda", generator=gen).half()
+    qw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    kw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    inv = ga.build_inv_freq(THETA).cuda()
+    q_out = torch.zeros(((hq + hkv), D), device="cuda", dtype=torch.float16)
+    attn_out = torch.zeros((hkv, G, D), device="cuda", dtype=torch.float16)
+    pos_t = torch.zeros((1,), device="cuda", dtype=torch.int32)
+    ns = ga.pick_num_splits(MS, hkv)
+    att, lse = ga.decode_scratch(hkv, G, ns)
+    scale_bits = int(torch.tensor([1.0 / math.sqrt(D)], dtype=torch.float16).view(torch.int16)
+                     .item()) & 0xFFFF
+    runner = ga.DecodeGraphRunner(
+        qkv=qkv, q_weight=qw, k_weight=kw, inv_freq=inv, q_out=q_out, k_cache=kc, v_cache=vc,
+        att_partial=att, lse_partial=lse, attn_out=attn_out, position=pos_t, eps=EPS,
+        qk_scale_f16_bits=scale_bits, num_q_heads=hq, num_kv_heads=hkv, num_splits=ns,
+        prime_position=ctx)
+    s = runner.stream
+    try:
+        for i in range(warmup):
+            runner.launch_step(ctx + i % replays)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        for i in range(replays):
+            runner.launch_step(ctx + i)
+        b.record(s)
+        torch.cuda.synchronize()
+        step_us = a.elapsed_time(b) * 1e3 / replays
+        assert torch.isfinite(attn_out).all().item(), "non-finite decode output"
+    finally:
+        runner.close()
+    # Bytes of the average replayed step (s_kv grows by one per replay).
+    avg_bytes = sum(decode_bytes(hq, hkv, ctx + i + 1) for i in range(replays)) / replays
+
+    # Split kernel alone, eager, position ctx (s_kv = ctx + 1).
+    q_grouped = q_out[:hq].view(hkv, G, D)
+    pos_t.fill_(ctx)
+    with torch.cuda.stream(s):
+        fn = lambda: ga.fmha_decode_gqa_split(q_grouped, kc, vc, att, lse, scale_bits, pos_t)  # noqa
+        durs, _ = time_launches(torch, fn, split_steps, 10, stream=s)
+        mfn = lambda: ga.splitk_reduce_merge(att, lse, attn_out)  # noqa: E731
+        mdurs, _ = time_launches(torch, mfn, split_steps, 10, stream=s)
+    split_us = 1e3 * sum(durs) / len(durs)
+    merge_us = 1e3 * sum(mdurs) / len(mdurs)
+    bytes_split = decode_bytes(hq, hkv, ctx + 1)
+    return dict(
+        hq=hq, hkv=hkv, ctx=ctx, num_splits=ns, replays=replays, step_us=step_us,
+        step_gbs=avg_bytes / (step_us * 1e-6) / 1e9, split_us=split_us, merge_us=merge_us,
+        split_gbs=bytes_split / (split_us * 1e-6) / 1e9, bytes_split=bytes_split,
+        kc=kc, vc=vc, q=q_out[:hq].clone())
+
+
+def cpu_baseline_prefill(torch, pre, threads: int):
+    """Oracle fp32 attention over every query row of the c3 inputs (about 10 s on 16 cores)."""
+    import oracle
+
+    q = pre["q"].cpu().numpy()
+    kc = pre["kc"].cpu().numpy()
+    vc = pre["vc"].cpu().numpy()
+    S, hq = pre["S"], pre["hq"]
+    step, begin = 1, 0
+    t0 = time.perf_counter()
+    oracle.attn_prefill_f32(q, kc, vc, 1.0 / math.sqrt(D), S, 0, row_begin=begin,
+                            row_step=step, nthreads=threads)
+    dt = time.perf_counter() - t0
+    rows = range(begin, S, step)
+    flops = sum(2.0 * 2.0 * D * hq * (m + 1) for m in rows)
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"c3 inputs, query rows {begin}::{step} ({len(rows)} of {S}) x {hq} "
+                       f"heads, {dt:.1f} s; oracle/grout_oracle.c go_attn_prefill_f32 "
+                       f"(fp32, two-pass softmax), OpenMP over (row, head)")
+
+
+def cpu_baseline_decode(torch, dec, threads: int):
+    import oracle
+
+    hq, hkv, ctx = dec["hq"], dec["hkv"], dec["ctx"]
+    q = dec["q"].cpu().numpy().reshape(1, hq, D)
+    kc = dec["kc"][:, :ctx + 1].contiguous().cpu().numpy()
+    vc = dec["vc"][:, :ctx + 1].contiguous().cpu().numpy()
+    t0 = time.perf_counter()
+    oracle.attn_prefill_f32(q, kc, vc, 0.08837890625, ctx + 1, ctx, nthreads=threads)
+    dt = time.perf_counter() - t0
+    return dict(value=decode_bytes(hq, hkv, ctx + 1) / dt / 1e9, unit="GB/s", cores=threads,
+                kind="port", sample=f"one c4 decode step (s_kv={ctx + 1}, {hq} heads), "
+                                    f"{dt * 1e3:.0f} ms, fp32 oracle")
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-replays", type=int, default=1000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(attention shards by KV head with no communication; see DESIGN.md).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import grout_amd as ga
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    ga.lib()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x67726F7574000003)
+
+    def log(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    log("prefill c3 ...")
+    pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
+    log(f"prefill c3: {pre['ms']:.3f} ms/launch, {pre['tflops']:.1f} TFLOP/s")
+    log("qk_norm_rope c3 ...")
+    nrm = bench_norm(torch, ga, args.steps, args.warmup, gen)
+    log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
+    log("decode c4 ...")
+    dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, 20, gen, 200)
+    log(f"decode c4: step {dec['step_us']:.2f} us ({dec['step_gbs']:.0f} GB/s), "
+        f"split {dec['split_us']:.2f} us ({dec['split_gbs']:.0f} GB/s), "
+        f"merge {dec['merge_us']:.2f} us, NKS={dec['num_splits']}")
+    log("decode c2 ...")
+    dec2 = bench_decode(torch, ga, 32, 8, 4096, 200, 20, gen, 200)
+    log(f"decode c2: step {dec2['step_us']:.2f} us, split {dec2['split_us']:.2f} us")
+
+    threads = min(16, os.cpu_count() or 1)
+    cpu = None
+    cpu_dec = None
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline ({threads} threads) ...")
+        cpu = cpu_baseline_prefill(torch, pre, threads)
+        cpu_dec = cpu_baseline_decode(torch, dec, threads)
+        log(f"cpu: {cpu['value'] * 1e3:.2f} GFLOP/s prefill, {cpu_dec['value']:.2f} GB/s decode")
+
+    def rl(bound, achieved, peak, unit, traffic=None):
+        return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": traffic}
+
+    line = {
+        "metric": METRIC,
+        "value": round(pre["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "c3: Qwen3-4B causal prefill attention, batch 1, S=8192, "
+                               "32 Q / 8 KV heads, head_dim 128, f16 (fp32 accumulation)",
+                   "seq_len": pre["S"], "num_q_heads": pre["hq"], "num_kv_heads": pre["hkv"],
+                   "head_dim": D, "flops_per_step": pre["flops"]},
+        "roofline": rl("mfma", pre["tflops"], PEAK_TFLOPS_F16, "TFLOP/s"),
+        "cpu_baseline": cpu,
+        "decode": {
+            "workload": "c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context 32768, "
+                        f"hipGraph x{dec['replays']} (norm/RoPE/KV write + split + merge)",
+            "value": round(dec["step_gbs"], 1), "unit": "GB/s",
+            "us_per_step": round(dec["step_us"], 3), "num_splits": dec["num_splits"],
+            "split_us": round(dec["split_us"], 3), "merge_us": round(dec["merge_us"], 3),
+            "roofline": rl("hbm", dec["split_gbs"], PEAK_HBM_GBS, "GB/s"),
+            "step_frac_of_hbm_peak": round(dec["step_gbs"] / PEAK_HBM_GBS, 4),
+            "cpu_baseline": cpu_dec,
+        },
+        "decode_c2": {"us_per_step": round(dec2["step_us"], 3),
+                      "split_us": round(dec2["split_us"], 3),
+                      "split_gbs": round(dec2["split_gbs"], 1),
+                      "num_splits": dec2["num_splits"]},
+        "qk_norm_rope_c3": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
+                            "frac_of_hbm_peak": round(nrm["gbs"] / PEAK_HBM_GBS, 4)},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
