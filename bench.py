@@ -157,21 +157,29 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
     # Bytes of the average replayed step (s_kv grows by one per replay).
     avg_bytes = sum(decode_bytes(hq, hkv, ctx + i + 1) for i in range(replays)) / replays
 
-    # Split kernel alone, eager, position ctx (s_kv = ctx + 1).
-    q_grouped = q_out[:hq].view(hkv, G, D)
+    # The fused step alone (the graph's only kernel), eager at position ctx
+    # (s_kv = ctx + 1, position not advanced), per-launch events; then the
+    # standalone split and merge ops of the same shape.
+    counters = ga.decode_counters(hkv)
     pos_t.fill_(ctx)
     with torch.cuda.stream(s):
+        ffn = lambda: ga.decode_fused(qkv, qw, kw, inv, q_out, kc, vc, att, lse, attn_out,  # noqa
+                                      counters, pos_t, EPS, scale_bits, hq, hkv)
+        fdurs, _ = time_launches(torch, ffn, split_steps, 10, stream=s)
+        q_grouped = q_out[:hq].view(hkv, G, D)
         fn = lambda: ga.fmha_decode_gqa_split(q_grouped, kc, vc, att, lse, scale_bits, pos_t)  # noqa
         durs, _ = time_launches(torch, fn, split_steps, 10, stream=s)
         mfn = lambda: ga.splitk_reduce_merge(att, lse, attn_out)  # noqa: E731
         mdurs, _ = time_launches(torch, mfn, split_steps, 10, stream=s)
+    fused_us = 1e3 * sum(fdurs) / len(fdurs)
     split_us = 1e3 * sum(durs) / len(durs)
     merge_us = 1e3 * sum(mdurs) / len(mdurs)
-    bytes_split = decode_bytes(hq, hkv, ctx + 1)
+    bytes_step = decode_bytes(hq, hkv, ctx + 1)
     return dict(
         hq=hq, hkv=hkv, ctx=ctx, num_splits=ns, replays=replays, step_us=step_us,
-        step_gbs=avg_bytes / (step_us * 1e-6) / 1e9, split_us=split_us, merge_us=merge_us,
-        split_gbs=bytes_split / (split_us * 1e-6) / 1e9, bytes_split=bytes_split,
+        step_gbs=avg_bytes / (step_us * 1e-6) / 1e9, fused_us=fused_us,
+        fused_gbs=bytes_step / (fused_us * 1e-6) / 1e9, split_us=split_us, merge_us=merge_us,
+        split_gbs=bytes_step / (split_us * 1e-6) / 1e9, bytes_step=bytes_step,
         kc=kc, vc=vc, q=q_out[:hq].clone())
 
 
@@ -248,12 +256,14 @@ def main(argv=None) -> int:
     log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
     log("decode c4 ...")
     dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, 20, gen, 200)
-    log(f"decode c4: step {dec['step_us']:.2f} us ({dec['step_gbs']:.0f} GB/s), "
+    log(f"decode c4: graph step {dec['step_us']:.2f} us ({dec['step_gbs']:.0f} GB/s), "
+        f"fused kernel {dec['fused_us']:.2f} us ({dec['fused_gbs']:.0f} GB/s), "
         f"split {dec['split_us']:.2f} us ({dec['split_gbs']:.0f} GB/s), "
         f"merge {dec['merge_us']:.2f} us, NKS={dec['num_splits']}")
     log("decode c2 ...")
     dec2 = bench_decode(torch, ga, 32, 8, 4096, 200, 20, gen, 200)
-    log(f"decode c2: step {dec2['step_us']:.2f} us, split {dec2['split_us']:.2f} us")
+    log(f"decode c2: graph step {dec2['step_us']:.2f} us, fused {dec2['fused_us']:.2f} us, "
+        f"split {dec2['split_us']:.2f} us")
 
     threads = min(16, os.cpu_count() or 1)
     cpu = None
@@ -289,17 +299,20 @@ def main(argv=None) -> int:
         "cpu_baseline": cpu,
         "decode": {
             "workload": "c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context 32768, "
-                        f"hipGraph x{dec['replays']} (norm/RoPE/KV write + split + merge)",
+                        f"hipGraph x{dec['replays']} of the fused step (norm/RoPE/KV write + "
+                        "split + merge, one kernel)",
             "value": round(dec["step_gbs"], 1), "unit": "GB/s",
             "us_per_step": round(dec["step_us"], 3), "num_splits": dec["num_splits"],
-            "split_us": round(dec["split_us"], 3), "merge_us": round(dec["merge_us"], 3),
-            "roofline": rl("hbm", dec["split_gbs"], PEAK_HBM_GBS, "GB/s"),
+            "fused_kernel_us": round(dec["fused_us"], 3),
+            "standalone_split_us": round(dec["split_us"], 3),
+            "standalone_merge_us": round(dec["merge_us"], 3),
+            "roofline": rl("hbm", dec["fused_gbs"], PEAK_HBM_GBS, "GB/s"),
             "step_frac_of_hbm_peak": round(dec["step_gbs"] / PEAK_HBM_GBS, 4),
             "cpu_baseline": cpu_dec,
         },
         "decode_c2": {"us_per_step": round(dec2["step_us"], 3),
-                      "split_us": round(dec2["split_us"], 3),
-                      "split_gbs": round(dec2["split_gbs"], 1),
+                      "fused_kernel_us": round(dec2["fused_us"], 3),
+                      "fused_gbs": round(dec2["fused_gbs"], 1),
                       "num_splits": dec2["num_splits"]},
         "qk_norm_rope_c3": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                             "frac_of_hbm_peak": round(nrm["gbs"] / PEAK_HBM_GBS, 4)},

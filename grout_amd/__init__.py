@@ -38,7 +38,8 @@ from ._lib import GROUT_OK, LibraryMissing
 __all__ = [
     "GroutError", "LibraryMissing", "lib", "build_inv_freq", "qk_norm_rope_kv_prefill",
     "qk_norm_rope_kv_decode", "attend_prefill", "fmha_decode_gqa_split",
-    "splitk_reduce_merge", "decode_scratch", "pick_num_splits", "DecodeGraphRunner",
+    "splitk_reduce_merge", "decode_fused", "decode_scratch", "decode_counters",
+    "pick_num_splits", "DecodeGraphRunner",
     "HEAD_DIM", "ATTN_BN_DECODE",
 ]
 
@@ -195,6 +196,38 @@ def decode_scratch(num_kv_heads: int, group: int, num_splits: int, head_dim: int
     return att, lse
 
 
+def decode_counters(num_kv_heads: int, device="cuda"):
+    """Zeroed merge counters for :func:`decode_fused`
+    (grout_attn_decode_counter_bytes bytes, int32 storage)."""
+    torch = _torch()
+    nbytes = int(lib().grout_attn_decode_counter_bytes(num_kv_heads))
+    return torch.zeros((nbytes // 4,), dtype=torch.int32, device=device)
+
+
+def decode_fused(qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache, att_partial,
+                 lse_partial, out, counters, position, eps: float, qk_scale_f16_bits: int,
+                 num_q_heads: int, num_kv_heads: int, block_n: int = ATTN_BN_DECODE,
+                 advance_position: bool = False):
+    """One decode step in one launch: the QK norm/RoPE/KV write, split-K GQA
+    attention and merge that grout records as three ops (src/model.rs:3194-3221,
+    3428-3473).  Writes q_out rows [0, Hq), the cache row at *position and out
+    [Hkv, G, D]; with advance_position the device position ends one higher."""
+    D = q_weight.shape[0]
+    G = num_q_heads // num_kv_heads
+    _ensure(qkv.numel() == (num_q_heads + 2 * num_kv_heads) * D, "qkv size mismatch")
+    _ensure(att_partial.dim() == 3 and att_partial.shape[1] % G == 0, "att_partial shape mismatch")
+    ns = att_partial.shape[1] // G
+    _ensure(counters.numel() * 4 >= lib().grout_attn_decode_counter_bytes(num_kv_heads),
+            "counters too small")
+    _check(lib().grout_attn_decode_fused(
+        _ptr(qkv), _ptr(q_weight), _ptr(k_weight), _ptr(inv_freq), _ptr(q_out), _ptr(k_cache),
+        _ptr(v_cache), _ptr(att_partial), _ptr(lse_partial), _ptr(out), _ptr(counters),
+        _ptr(position), float(eps), int(qk_scale_f16_bits), num_q_heads, num_kv_heads, D,
+        k_cache.shape[1], block_n, ns, 1 if advance_position else 0, _stream()),
+        "decode_fused")
+    return out
+
+
 def fmha_decode_gqa_split(q_grouped, k_cache, v_cache, att_partial, lse_partial,
                           qk_scale_f16_bits: int, position, block_n: int = ATTN_BN_DECODE):
     """fmha_decode_gqa_split as recorded at src/model.rs:3428-3452; q_grouped [Hkv, G, D]."""
@@ -222,25 +255,31 @@ def splitk_reduce_merge(att_partial, lse_partial, out):
 class DecodeGraphRunner:
     """Attention slice of DecodeCudaGraphRunner (src/model.rs:318-493).
 
-    Captures {fused norm/RoPE/KV write, split-K decode, merge} for one layer's
-    buffers into a hipGraph; :meth:`launch_step` rewrites the device position
-    and replays it (no host sync)."""
+    Captures the fused decode step (norm/RoPE/KV write, split-K decode, merge)
+    for one layer's buffers into a hipGraph; :meth:`launch_step` makes the
+    device position the requested one and replays it (no host sync).  The
+    graph advances the position itself, so consecutive steps write nothing."""
 
     def __init__(self, *, qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache,
                  att_partial, lse_partial, attn_out, position, eps: float,
                  qk_scale_f16_bits: int, num_q_heads: int, num_kv_heads: int,
                  num_splits: int, block_n: int = ATTN_BN_DECODE, prime_position: int = 0,
-                 stream=None):
+                 counters=None, stream=None):
         torch = _torch()
+        if counters is None:
+            counters = decode_counters(num_kv_heads, device=k_cache.device)
+        self.counters = counters
         self._keep = (qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache, att_partial,
-                      lse_partial, attn_out, position)
+                      lse_partial, attn_out, position, counters)
         self.stream = stream if stream is not None else torch.cuda.Stream()
+        torch.cuda.current_stream().synchronize()  # caller's buffers are ready
         L = _lib.DecodeLayer(
             qkv=_ptr(qkv), q_weight=_ptr(q_weight), k_weight=_ptr(k_weight),
             inv_freq=_ptr(inv_freq), q_out=_ptr(q_out), k_cache=_ptr(k_cache),
             v_cache=_ptr(v_cache), att_partial=_ptr(att_partial),
             lse_partial=_ptr(lse_partial), attn_out=_ptr(attn_out),
-            d_position=_ptr(position), eps=float(eps), qk_scale_f16=int(qk_scale_f16_bits),
+            d_position=_ptr(position), counters=_ptr(counters), eps=float(eps),
+            qk_scale_f16=int(qk_scale_f16_bits),
             num_q_heads=num_q_heads, num_kv_heads=num_kv_heads, head_dim=q_weight.shape[0],
             max_seq_len=k_cache.shape[1], block_n=block_n, num_splits=num_splits)
         self._layer = L

@@ -41,7 +41,7 @@ class DecodeLayer(ctypes.Structure):
         ("qkv", c_vp), ("q_weight", c_vp), ("k_weight", c_vp), ("inv_freq", c_vp),
         ("q_out", c_vp), ("k_cache", c_vp), ("v_cache", c_vp), ("att_partial", c_vp),
         ("lse_partial", c_vp), ("attn_out", c_vp), ("d_position", c_vp),
-        ("eps", c_f32), ("qk_scale_f16", c_u16), ("num_q_heads", c_i32),
+        ("counters", c_vp), ("eps", c_f32), ("qk_scale_f16", c_u16), ("num_q_heads", c_i32),
         ("num_kv_heads", c_i32), ("head_dim", c_i32), ("max_seq_len", c_i32),
         ("block_n", c_i32), ("num_splits", c_i32),
     ]
@@ -59,6 +59,9 @@ SIGNATURES = {
     "grout_attn_decode_split": (
         c_i32, [c_vp] * 5 + [c_u16, c_vp] + [c_i32] * 6 + [c_vp]),
     "grout_attn_decode_merge": (c_i32, [c_vp] * 3 + [c_i32] * 4 + [c_vp]),
+    "grout_attn_decode_fused": (
+        c_i32, [c_vp] * 12 + [c_f32, c_u16] + [c_i32] * 7 + [c_vp]),
+    "grout_attn_decode_counter_bytes": (c_i64, [c_i32]),
     "grout_attn_decode_partial_bytes": (c_i64, [c_i32] * 4),
     "grout_attn_decode_lse_bytes": (c_i64, [c_i32] * 3),
     "grout_attn_decode_pick_splits": (c_i32, [c_i32] * 4),

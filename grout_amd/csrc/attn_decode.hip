@@ -1,29 +1,41 @@
-// Split-K GQA decode attention and its log-sum-exp merge.
+// Split-K GQA decode attention, its log-sum-exp merge, and the fused decode
+// step (QK norm/RoPE/KV write + split + merge in one launch).
 //
-// Replaces fmha_decode_gqa_split (src/kernels.rs:2586-2749) and
-// splitk_reduce_merge (src/kernels.rs:2771-2868).  The scratch layout, the
-// split boundaries and the per-split numerics are the reference's:
+// Replaces fmha_decode_gqa_split (src/kernels.rs:2586-2749),
+// splitk_reduce_merge (src/kernels.rs:2771-2868) and, in the fused form, the
+// qk_norm_rope_kv_decode_raw_f16 -> fmha_decode_gqa_split -> splitk_reduce_merge
+// sequence grout records per layer (src/model.rs:3194-3221, 3428-3473).
+// The scratch layout, the split boundaries and the per-split numerics are the
+// reference's:
 //   s_kv = pos + 1; tiles = ceil(s_kv/BN); per = ceil(tiles/NKS);
 //   split s covers tokens [s*per*BN, min((s*per+per)*BN, s_kv));
 //   O_s = f16(acc/max(l,1e-8)), LSE_s = m + log2(max(l,1e-8)) in log2 units,
 //   att_partial [Hkv, NKS*G, D] split-major, lse_partial [Hkv, NKS*G].
 //
-// Decode is HBM-bound (4-8 FLOP per byte), so the kernel is shaped for bytes
-// in flight, not for arithmetic:
-//  * Workgroup = (split, kv_head), 4 wavefronts.  Each wavefront walks
-//    32-token sub-tiles of the split (wave w takes sub-tiles w, w+4, ...),
-//    prefetching the next sub-tile's K and V (16 KB) into registers while the
-//    current one is computed.
-//  * All G query heads of the KV head share every K/V byte: S^T = K Q^T and
-//    O^T += V^T P^T run on v_mfma_f32_16x16x32_f16 with the G heads (padded
-//    to 16) as the N dimension.  K rows feed the A operand straight from
-//    16-byte global loads; Q^T is held in registers for the whole split.
-//  * The S^T accumulator layout is reused as the P^T operand of the PV
-//    product (no data movement): the reduction slots of lane group q are the
-//    tokens {4q..4q+3, 16+4q..16+4q+3} of the sub-tile.  V^T is produced in
-//    the same slot order by parking the V sub-tile in a per-wave LDS buffer
-//    and reading it back with ds_read_b64_tr_b16 (gfx950 transposing read).
+// Decode is HBM-bound (4-8 FLOP per byte); the kernel is shaped for bytes in
+// flight:
+//  * Workgroup = (split, kv_head), 4 wavefronts, one per CU (LDS-bound).
+//    The split's tokens stream through LDS in 64-token chunks (K 16 KB +
+//    V 16 KB) with direct HBM->LDS copies over 4 stages: after the one
+//    barrier per chunk the next-but-two chunk is issued, so ~96-128 KB per
+//    CU are in flight while a chunk is computed, without staging registers.
+//  * Each wavefront takes 16 tokens of a chunk.  All G query heads of the KV
+//    head share every K/V byte: S^T = K Q^T runs on v_mfma_f32_16x16x32_f16
+//    and O^T += V^T P^T on v_mfma_f32_16x16x16_f16 with the G heads (padded to
+//    16) as N.  The S^T accumulator layout is exactly the P^T operand
+//    (reduction slot j of lane group q is token 4q+j); V^T is read in the same
+//    order with one ds_read_b64_tr_b16 per 16 dims.
+//  * LDS rows are interleaved (token t in block t%16, row t/16) with padded
+//    block strides, so the operand reads are bank-conflict free and every
+//    read address is a per-lane base plus an immediate.
 //  * The four wavefronts' (m, l, acc) are combined through LDS at the end.
+//  * Fused form: every workgroup recomputes its G query rows (RMSNorm +
+//    RoPE, as the prefill/decode norm kernel); the split holding the new
+//    position also writes its K/V row to the cache before streaming.  The
+//    last workgroup of a KV head merges the splits, found with a counter;
+//    the partials travel through agent-coherent (sc1) stores and loads so no
+//    L2-wide writeback/invalidate is needed; the last head advances the
+//    device position when asked to.
 #include <math.h>
 
 #include "abi_util.h"
@@ -33,16 +45,27 @@ namespace grout {
 
 constexpr int kDecWaves = 4;
 constexpr int kDecThreads = kDecWaves * kWave;
-constexpr int kDecSub = 32;                 // tokens per wavefront iteration
-constexpr int kDecVStride = kHeadDim + 16;  // halves per LDS V row (288 B: spreads banks)
-constexpr int kDecVWaveBytes = kDecSub * kDecVStride * 2;
-constexpr int kDecRedBytes = kDecWaves * (16 * kHeadDim + 32) * 4;
-constexpr int kDecLdsBytes =
-    (kDecWaves * kDecVWaveBytes > kDecRedBytes) ? kDecWaves * kDecVWaveBytes : kDecRedBytes;
+constexpr int kDecSub = 16;                     // tokens per wavefront per chunk
+constexpr int kDecChunk = kDecWaves * kDecSub;  // 64 tokens per chunk
+constexpr int kDecKBlock = 4 * 256 + 16;        // 4 rows of 256 B + pad (K)
+constexpr int kDecVBlock = 4 * 256 + 32;        // 4 rows of 256 B + pad (V)
+constexpr int kDecKBytes = 16 * kDecKBlock;
+constexpr int kDecVBytes = 16 * kDecVBlock;
+constexpr int kDecStageBytes = kDecKBytes + kDecVBytes;
+constexpr int kDecStages = 4;
+constexpr int kDecDmaPerWave = 16 / kDecWaves;  // 1 KB copies of K (and of V) per wave
+constexpr int kDecRedStride = 16 * kHeadDim + 32;   // floats per wave in the final combine
 constexpr float kNegBig = -1.0e30f;
+// Merge counters sit in separate 256-byte lines so the heads' atomics do not
+// serialise on one line.
+constexpr int kDecCounterStride = 64;  // u32 elements
 
-struct DecodeSplitArgs {
-    const uint16_t* q;
+static_assert(kDecWaves * kDecRedStride * 4 <= kDecStages * kDecStageBytes,
+              "wave combine reuses the stage buffers");
+
+struct DecodeArgs {
+    // Attention (all forms).
+    const uint16_t* q;          // [Hkv, G, D] rotated queries (split-only form)
     const uint16_t* k_cache;
     const uint16_t* v_cache;
     uint16_t* att_partial;
@@ -50,26 +73,151 @@ struct DecodeSplitArgs {
     const uint32_t* d_position;
     float scale_log2;
     int group;
+    int num_kv_heads;
     int max_seq_len;
     int block_n;
     int num_splits;
+    // Fused form only.
+    const uint16_t* qkv;        // [Q(Hq*D) | K(Hkv*D) | V(Hkv*D)]
+    const uint16_t* q_weight;
+    const uint16_t* k_weight;
+    const float* inv_freq;
+    uint16_t* q_out;            // rows [0, Hq) written
+    uint16_t* k_cache_w;        // = k_cache, writable
+    uint16_t* v_cache_w;        // = v_cache, writable
+    uint16_t* out;              // [Hkv, G, D]
+    uint32_t* counters;         // Hkv + 1 counters kDecCounterStride apart, zero on entry and exit
+    uint32_t* position_w;       // = d_position, advanced when advance_position
+    float eps;
+    int num_q_heads;
+    int advance_position;
 };
 
-__device__ __forceinline__ half8_t zero_half8() { return half8_t{}; }
+// Asynchronous 16-byte HBM -> LDS copy (global_load_lds_dwordx4, scalar base
+// + 32-bit per-lane byte offset); lane l's 16 bytes land at LDS byte
+// lds_base + 16*l.  Inline asm keeps the compiler from serialising the copies
+// behind vmcnt(0) waits; the kernel waits for them with s_waitcnt vmcnt before
+// its workgroup barrier.  M0 carries the LDS base; one wait state separates
+// the M0 write from the copy.
+__device__ __forceinline__ void dec_lds_dma16(const void* gbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff), "s"(gbase), "s"(lds_base)
+        : "memory");
+}
 
-__global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(DecodeSplitArgs a) {
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kDecLdsBytes];
+// Same copy with a full 64-bit per-lane source address.
+__device__ __forceinline__ void dec_lds_dma16_ptr(const void* gptr, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, off"
+        :
+        : "v"(gptr), "s"(lds_base)
+        : "memory");
+}
+
+constexpr int dec_waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
+// Per-workgroup inputs staged into LDS ahead of the K/V stream, 256 B rows:
+// split-only form: rows [0,G) = the G rotated query rows; fused form: rows
+// [0,G) = raw query rows of the QKV vector, then K row, V row, q_weight,
+// k_weight and inv_freq (64 f32 = 256 B).
+constexpr int kDecProRows = GROUT_MAX_DECODE_GROUP + 5;
+constexpr int kDecProDmas = (kDecProRows + 3) / 4;
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+// RMSNorm + RoPE of one 128-wide row held by 8 lanes (lane t: elements
+// [8t,8t+8) and [64+8t, 64+8t+8)), same operation order as
+// qk_norm_rope_kv_kernel.
+__device__ __forceinline__ void norm_rope_row8(half8_t xlo, half8_t xhi, half8_t wlo, half8_t whi,
+                                               const float* s_cos, const float* s_sin, float eps,
+                                               int lane8, half8_t& ylo, half8_t& yhi) {
+#pragma clang fp contract(off)
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float a = static_cast<float>(xlo[i]);
+        const float b = static_cast<float>(xhi[i]);
+        ss += a * a + b * b;
+    }
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    const float inv_rms = 1.0f / sqrtf(ss / 128.0f + eps);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float n_lo = static_cast<float>(xlo[i]) * inv_rms * static_cast<float>(wlo[i]);
+        const float n_hi = static_cast<float>(xhi[i]) * inv_rms * static_cast<float>(whi[i]);
+        const float cv = s_cos[8 * lane8 + i];
+        const float sv = s_sin[8 * lane8 + i];
+        ylo[i] = static_cast<half_t>(n_lo * cv - n_hi * sv);
+        yhi[i] = static_cast<half_t>(n_hi * cv + n_lo * sv);
+    }
+}
+
+// Workgroup barrier that waits only for this wave's LDS traffic: copies into
+// LDS stay in flight across it.  The asm memory clobber keeps the compiler
+// from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Agent-coherent (sc1) 16-byte store / load as four relaxed agent-scope
+// 32-bit atomics: visible to a workgroup on another XCD without an L2-wide
+// writeback or invalidate.
+__device__ __forceinline__ void store16_agent(uint16_t* p, half8_t v) {
+    const uint4_t u = __builtin_bit_cast(uint4_t, v);
+    uint32_t* q = reinterpret_cast<uint32_t*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) __hip_atomic_store(q + i, u[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ half8_t load16_agent(const uint16_t* p) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    uint4_t u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = __hip_atomic_load(q + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_bit_cast(half8_t, u);
+}
+
+__device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+template <bool kFused>
+__global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs a) {
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kDecStages * kDecStageBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char pro[kDecProDmas * 1024];
+    __shared__ __attribute__((aligned(16))) half_t q_lds[GROUT_MAX_DECODE_GROUP * kHeadDim];
+    __shared__ float s_cos[64], s_sin[64];
+    __shared__ uint32_t s_flag;
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
-    const int wave = threadIdx.x / kWave;
-    const int lane = threadIdx.x % kWave;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid % kWave;
     const int n = lane & 15;     // head column of the MFMA tiles
     const int qgrp = lane >> 4;  // lane group: k-slice / token quartet
+    const int G = a.group;
 
-    // Position from device memory; clamped so no read leaves the cache.
-    uint32_t pos = *a.d_position;
-    if (pos >= static_cast<uint32_t>(a.max_seq_len)) pos = a.max_seq_len - 1;
+    // Position from device memory; reads are clamped to the cache.
+    const uint32_t pos_raw = *a.d_position;
+    const uint32_t pos = pos_raw < static_cast<uint32_t>(a.max_seq_len) ? pos_raw
+                                                                         : a.max_seq_len - 1;
     const int s_kv = static_cast<int>(pos) + 1;
     const int tiles = (s_kv + a.block_n - 1) / a.block_n;
     const int per = (tiles + a.num_splits - 1) / a.num_splits;
@@ -77,19 +225,159 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(DecodeSp
     const int te = min(tb + per, tiles);
     const int tok_begin = tb * a.block_n;
     const int tok_end = (tb < te) ? min(te * a.block_n, s_kv) : tok_begin;
+    const int nchunks = (tok_end - tok_begin + kDecChunk - 1) / kDecChunk;
+
+    const uint16_t* kh = a.k_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
+    const uint16_t* vh = a.v_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
+
+    // Chunk copy: K/V block b (tokens b + 16*row, rows 0..3) of a chunk is one
+    // 1 KB copy; this wavefront moves blocks 4*wave..4*wave+3.  Lane l covers
+    // row l/16, 16-byte column l%16.  Rows at or past tok_end are clamped to
+    // tok_end-1 (their scores are masked).
+    const uint32_t lds0 = static_cast<uint32_t>(
+        (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(lds)));
+    const uint32_t lane_off = 4096u * static_cast<uint32_t>(lane >> 4) + 16u * (lane & 15);
+    auto issue_chunk = [&](int c) {
+        const uint32_t kb = lds0 + (c % kDecStages) * kDecStageBytes;
+        const uint32_t vb = kb + kDecKBytes;
+        const int t0 = tok_begin + c * kDecChunk;
+        const bool clamp = t0 + kDecChunk > tok_end;
+#pragma unroll
+        for (int r = 0; r < kDecDmaPerWave; ++r) {
+            const int blk = kDecDmaPerWave * wave + r;
+            int64_t row_base = static_cast<int64_t>(t0 + blk) * kHeadDim;
+            uint32_t off = lane_off;
+            if (clamp) {
+                const int tok = min(t0 + blk + 16 * (lane >> 4), tok_end - 1);
+                row_base = static_cast<int64_t>(t0) * kHeadDim;  // tok >= t0: offset stays >= 0
+                off = static_cast<uint32_t>(tok - t0) * 256u + 16u * (lane & 15);
+            }
+            dec_lds_dma16(kh + row_base, off, kb + kDecKBlock * blk);
+            dec_lds_dma16(vh + row_base, off, vb + kDecVBlock * blk);
+        }
+    };
+
+    // Prologue inputs into `pro` (wave 0), then the first K/V chunks (all
+    // waves); nothing waits on an ordinary load, so the copies go out at once.
+    const uint32_t pro0 = static_cast<uint32_t>(
+        (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(pro)));
+    const int n_pro = kFused ? G + 5 : G;
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < kDecProDmas; ++i) {
+            if (4 * i < n_pro) {
+                int r = 4 * i + (lane >> 4);
+                if (r >= n_pro) r = 0;  // pad lanes repeat row 0
+                const unsigned char* src;
+                if constexpr (kFused) {
+                    const int64_t hq = a.num_q_heads, hkv = a.num_kv_heads;
+                    if (r < G) {
+                        src = reinterpret_cast<const unsigned char*>(a.qkv + (static_cast<int64_t>(kvh) * G + r) * kHeadDim);
+                    } else if (r == G) {
+                        src = reinterpret_cast<const unsigned char*>(a.qkv + (hq + kvh) * kHeadDim);
+                    } else if (r == G + 1) {
+                        src = reinterpret_cast<const unsigned char*>(a.qkv + (hq + hkv + kvh) * kHeadDim);
+                    } else if (r == G + 2) {
+                        src = reinterpret_cast<const unsigned char*>(a.q_weight);
+                    } else if (r == G + 3) {
+                        src = reinterpret_cast<const unsigned char*>(a.k_weight);
+                    } else {
+                        src = reinterpret_cast<const unsigned char*>(a.inv_freq);
+                    }
+                } else {
+                    src = reinterpret_cast<const unsigned char*>(a.q + (static_cast<int64_t>(kvh) * G + r) * kHeadDim);
+                }
+                dec_lds_dma16_ptr(src + 16 * (lane & 15), pro0 + 1024u * i);
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < kDecStages; ++c)
+        if (c < nchunks) issue_chunk(c);
+    // Wave 0's prologue copies are older than its chunk copies (8 per chunk).
+    if (wave == 0) {
+        const int later = min(kDecStages, nchunks);
+        if (later >= 4) {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(8 * kDecDmaPerWave));
+        } else if (later == 3) {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(6 * kDecDmaPerWave));
+        } else if (later == 2) {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(4 * kDecDmaPerWave));
+        } else if (later == 1) {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(2 * kDecDmaPerWave));
+        } else {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
+        }
+    }
+
+    // The split holding the new position (fused form) keeps the rotated K row
+    // and the V row in registers and patches them into its LDS chunk.
+    const bool owns_new_row = kFused && (tok_end == s_kv) && (tok_begin < tok_end) &&
+                              pos_raw < static_cast<uint32_t>(a.max_seq_len);
+    half8_t knew_lo{}, knew_hi{}, vnew_lo{}, vnew_hi{};
+    if constexpr (kFused) {
+        if (tid < 64) {
+            // f32 angle as the reference computes it; sin/cos correctly
+            // rounded to f32 via f64 (as qk_norm_rope_kv_kernel).
+            const float inv_f = *reinterpret_cast<const float*>(pro + (G + 4) * 256 + 4 * tid);
+            const float theta = static_cast<float>(static_cast<int>(pos_raw)) * inv_f;
+            double sv, cv;
+            sincos(static_cast<double>(theta), &sv, &cv);
+            s_cos[tid] = static_cast<float>(cv);
+            s_sin[tid] = static_cast<float>(sv);
+        }
+        lds_barrier();  // also publishes `pro`
+        const int row = tid >> 3, lane8 = tid & 7;
+        const bool do_q = row < G;
+        const bool do_k = row == G && owns_new_row;
+        if (do_q || do_k) {
+            const unsigned char* x = pro + row * 256;
+            const unsigned char* w = pro + (do_q ? G + 2 : G + 3) * 256;
+            half8_t ylo, yhi;
+            norm_rope_row8(*reinterpret_cast<const half8_t*>(x + 16 * lane8),
+                           *reinterpret_cast<const half8_t*>(x + 128 + 16 * lane8),
+                           *reinterpret_cast<const half8_t*>(w + 16 * lane8),
+                           *reinterpret_cast<const half8_t*>(w + 128 + 16 * lane8), s_cos, s_sin,
+                           a.eps, lane8, ylo, yhi);
+            if (do_q) {
+                *reinterpret_cast<half8_t*>(q_lds + row * kHeadDim + 8 * lane8) = ylo;
+                *reinterpret_cast<half8_t*>(q_lds + row * kHeadDim + 64 + 8 * lane8) = yhi;
+                if (split == 0) {
+                    uint16_t* qo = a.q_out + static_cast<int64_t>(kvh * G + row) * kHeadDim;
+                    store_half8(qo + 8 * lane8, ylo);
+                    store_half8(qo + 64 + 8 * lane8, yhi);
+                }
+            } else {
+                const unsigned char* vsrc = pro + (G + 1) * 256;
+                knew_lo = ylo;
+                knew_hi = yhi;
+                vnew_lo = *reinterpret_cast<const half8_t*>(vsrc + 16 * lane8);
+                vnew_hi = *reinterpret_cast<const half8_t*>(vsrc + 128 + 16 * lane8);
+                const int64_t slot = (static_cast<int64_t>(kvh) * a.max_seq_len + pos) * kHeadDim;
+                store_half8(a.k_cache_w + slot + 8 * lane8, ylo);
+                store_half8(a.k_cache_w + slot + 64 + 8 * lane8, yhi);
+                store_half8(a.v_cache_w + slot + 8 * lane8, vnew_lo);
+                store_half8(a.v_cache_w + slot + 64 + 8 * lane8, vnew_hi);
+            }
+        }
+        lds_barrier();
+    } else {
+        lds_barrier();  // publishes `pro`
+    }
 
     // Q^T as the B operand: lane holds head n, dims 32c + 8*qgrp + [0,8).
     half8_t qop[4];
     {
-        const uint16_t* qh = a.q + (static_cast<int64_t>(kvh) * a.group + n) * kHeadDim;
+        const half_t* qsrc = kFused ? q_lds : reinterpret_cast<const half_t*>(pro);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            qop[c] = (n < a.group) ? load_half8(qh + 32 * c + 8 * qgrp) : zero_half8();
+            qop[c] = (n < G) ? *reinterpret_cast<const half8_t*>(qsrc + n * kHeadDim + 32 * c + 8 * qgrp)
+                             : half8_t{};
     }
-
-    const uint16_t* kh = a.k_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
-    const uint16_t* vh = a.v_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
-    half_t* vl = reinterpret_cast<half_t*>(lds + wave * kDecVWaveBytes);
+    // Chunk and slot of the new position within this split (owner only).
+    const int pos_local = static_cast<int>(pos) - tok_begin;
+    const int c_pos = owns_new_row ? pos_local / kDecChunk : -1;
+    const int t_pos = pos_local % kDecChunk;
 
     float m = kNegBig;
     float l = 0.0f;
@@ -97,97 +385,93 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(DecodeSp
 #pragma unroll
     for (int db = 0; db < 8; ++db) acc[db] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    // Register prefetch of one sub-tile: K as A operands, V as 8 rows-quartets.
-    half8_t kop[2][4], vreg[8];
-    auto fetch = [&](int t) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-            const int tok = t + 16 * mb + n;
-            const bool ok = tok < tok_end;
-            const uint16_t* kr = kh + static_cast<int64_t>(ok ? tok : tok_begin) * kHeadDim;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) kop[mb][c] = ok ? load_half8(kr + 32 * c + 8 * qgrp) : zero_half8();
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int tok = t + 4 * i + qgrp;
-            const bool ok = tok < tok_end;
-            vreg[i] = ok ? load_half8(vh + static_cast<int64_t>(tok) * kHeadDim + 8 * n) : zero_half8();
-        }
-    };
+    // Per-lane LDS read offsets within a stage.  K (A operand): token
+    // 16*wave + n -> block n, row wave; dims 32c + 8*qgrp.  V^T (transposing
+    // read, 16-lane group qgrp): tokens 16*wave + 4*qgrp + j -> block
+    // 4*qgrp + j, row wave; dims 16db + 4(lane%4).
+    const uint32_t k_lane = n * kDecKBlock + wave * 256 + 16 * qgrp;
+    const uint32_t v_lane = (4 * qgrp + (n >> 2)) * kDecVBlock + wave * 256 + 8 * (n & 3);
 
-    int t = tok_begin + kDecSub * wave;
-    if (t < tok_end) fetch(t);
-    for (; t < tok_end; t += kDecSub * kDecWaves) {
-        half8_t kcur[2][4], vcur[8];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) kcur[mb][c] = kop[mb][c];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vcur[i] = vreg[i];
-        const int tn = t + kDecSub * kDecWaves;
-        if (tn < tok_end) fetch(tn);
-
-        // S^T[token, head] for 32 tokens: lane holds head n, tokens
-        // t + 16*mb + 4*qgrp + r.
-        float4_t s[2];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-            s[mb] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) s[mb] = mfma16x16x32(kcur[mb][c], qop[c], s[mb]);
+    for (int c = 0; c < nchunks; ++c) {
+        // Chunk c has landed once only the copies of the chunks issued after
+        // it (8 per wave each; up to three) are outstanding.
+        const int younger = min(kDecStages - 1, nchunks - 1 - c);
+        if (younger >= 3) {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(6 * kDecDmaPerWave));
+        } else if (younger == 2) {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(4 * kDecDmaPerWave));
+        } else if (younger == 1) {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(2 * kDecDmaPerWave));
+        } else {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
         }
-        float mx = kNegBig;
+        lds_barrier();
+        // Every wavefront is past chunk c-1, whose stage now takes chunk c+3
+        // (chunks 0..3 were issued before the loop).
+        if (c >= 1 && c + kDecStages - 1 < nchunks) issue_chunk(c + kDecStages - 1);
+        if (c == c_pos) {
+            // The copy of this chunk read the cache before the new row was
+            // stored; put the new K/V row into its LDS slot.
+            const int row = tid >> 3, lane8 = tid & 7;
+            if (row == G) {
+                unsigned char* kb = lds + (c % kDecStages) * kDecStageBytes;
+                unsigned char* kr = kb + (t_pos & 15) * kDecKBlock + (t_pos >> 4) * 256;
+                unsigned char* vr = kb + kDecKBytes + (t_pos & 15) * kDecVBlock + (t_pos >> 4) * 256;
+                *reinterpret_cast<half8_t*>(kr + 16 * lane8) = knew_lo;
+                *reinterpret_cast<half8_t*>(kr + 128 + 16 * lane8) = knew_hi;
+                *reinterpret_cast<half8_t*>(vr + 16 * lane8) = vnew_lo;
+                *reinterpret_cast<half8_t*>(vr + 128 + 16 * lane8) = vnew_hi;
+            }
+            lds_barrier();
+        }
+
+        const int t = tok_begin + c * kDecChunk + kDecSub * wave;  // this wave's first token
+        if (t < tok_end) {
+            const unsigned char* kb = lds + (c % kDecStages) * kDecStageBytes;
+            const unsigned char* vb = kb + kDecKBytes;
+            // S^T[token, head]: lane holds head n, tokens t + 4qgrp + r.
+            float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+            for (int cc = 0; cc < 4; ++cc) {
+                const half8_t ka = *reinterpret_cast<const half8_t*>(kb + k_lane + 64 * cc);
+                s = mfma16x16x32(ka, qop[cc], s);
+            }
+            float mx = kNegBig;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int tok = t + 16 * mb + 4 * qgrp + r;
-                const float x = (tok < tok_end) ? s[mb][r] * a.scale_log2 : kNegBig;
-                s[mb][r] = x;
+                const int tok = t + 4 * qgrp + r;
+                const float x = (tok < tok_end) ? s[r] * a.scale_log2 : kNegBig;
+                s[r] = x;
                 mx = fmaxf(mx, x);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, swap_halves(mx));
-        const float m_new = fmaxf(m, mx);
-        const float alpha = exp2f(m - m_new);
-        float psum = 0.0f;
-        half8_t pop;
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, swap_halves(mx));
+            const float m_new = fmaxf(m, mx);
+            const float alpha = exp2f(m - m_new);
+            float psum = 0.0f;
+            half4_t pop;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = exp2f(s[mb][r] - m_new);
+                const float p = exp2f(s[r] - m_new);
                 psum += p;
-                pop[4 * mb + r] = static_cast<half_t>(p);
+                pop[r] = static_cast<half_t>(p);
             }
-        l = l * alpha + psum;
-        m = m_new;
+            l = l * alpha + psum;
+            m = m_new;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) acc[db] *= alpha;
-
-        // Park V rows t+4i+qgrp (dims 8n..8n+7) in LDS, read back transposed.
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            *reinterpret_cast<half8_t*>(vl + (4 * i + qgrp) * kDecVStride + 8 * n) = vcur[i];
-        wave_lds_sync();
-        const half_t* vr0 = vl + (4 * qgrp + (n >> 2)) * kDecVStride + 4 * (n & 3);
-        const half_t* vr1 = vr0 + 16 * kDecVStride;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            const half8_t vop = cat(lds_read_tr16(vr0 + 16 * db), lds_read_tr16(vr1 + 16 * db));
-            acc[db] = mfma16x16x32(vop, pop, acc[db]);
+            for (int db = 0; db < 8; ++db) {
+                const half4_t vop = lds_read_tr16(reinterpret_cast<const half_t*>(vb + v_lane + 32 * db));
+                acc[db] = mfma16x16x16(vop, pop, acc[db] * alpha);
+            }
         }
-        wave_lds_sync();
     }
 
     // Combine the wavefronts: per head M = max m_w, L = sum l_w 2^(m_w-M),
     // O = sum acc_w 2^(m_w-M) / max(L, 1e-8).
     l += __shfl_xor(l, 16);
     l += swap_halves(l);
-    __syncthreads();  // V buffers are reused for the reduction
-    float* red = reinterpret_cast<float*>(lds) + wave * (16 * kHeadDim + 32);
+    lds_barrier();  // stage buffers are reused for the combine
+    float* red = reinterpret_cast<float*>(lds) + wave * kDecRedStride;
     if (qgrp == 0) {
         red[16 * kHeadDim + n] = m;
         red[16 * kHeadDim + 16 + n] = l;
@@ -196,42 +480,165 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(DecodeSp
     for (int db = 0; db < 8; ++db)
 #pragma unroll
         for (int r = 0; r < 4; ++r) red[n * kHeadDim + 16 * db + 4 * qgrp + r] = acc[db][r];
-    __syncthreads();
+    lds_barrier();
 
-    const int g = threadIdx.x >> 4;        // head handled by this thread
-    const int d0 = (threadIdx.x & 15) * 8;  // 8 output dims
-    if (g < a.group) {
-        const float* base = reinterpret_cast<const float*>(lds);
-        const int wstride = 16 * kHeadDim + 32;
-        float M = kNegBig;
+    {
+        const int g = tid >> 4;        // head handled by this thread
+        const int d0 = (tid & 15) * 8; // 8 output dims
+        if (g < G) {
+            const float* base = reinterpret_cast<const float*>(lds);
+            float M = kNegBig;
 #pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, base[w * wstride + 16 * kHeadDim + g]);
-        float L = 0.0f, f[kDecWaves];
+            for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, base[w * kDecRedStride + 16 * kHeadDim + g]);
+            float L = 0.0f, f[kDecWaves];
 #pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) {
-            f[w] = exp2f(base[w * wstride + 16 * kHeadDim + g] - M);
-            L += base[w * wstride + 16 * kHeadDim + 16 + g] * f[w];
+            for (int w = 0; w < kDecWaves; ++w) {
+                f[w] = exp2f(base[w * kDecRedStride + 16 * kHeadDim + g] - M);
+                L += base[w * kDecRedStride + 16 * kHeadDim + 16 + g] * f[w];
+            }
+            const float l_safe = fmaxf(L, 1.0e-8f);
+            half8_t o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float x = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kDecWaves; ++w) x += base[w * kDecRedStride + g * kHeadDim + d0 + e] * f[w];
+                o[e] = static_cast<half_t>(x / l_safe);
+            }
+            const int64_t prow = (static_cast<int64_t>(kvh) * a.num_splits + split) * G + g;
+            const float lse_v = M + log2f(l_safe);
+            if constexpr (kFused) {
+                store16_agent(a.att_partial + prow * kHeadDim + d0, o);
+                if (d0 == 0)
+                    __hip_atomic_store(a.lse_partial + prow, lse_v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                store_half8(a.att_partial + prow * kHeadDim + d0, o);
+                if (d0 == 0) a.lse_partial[prow] = lse_v;
+            }
         }
-        const float l_safe = fmaxf(L, 1.0e-8f);
-        half8_t o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float x = 0.0f;
-#pragma unroll
-            for (int w = 0; w < kDecWaves; ++w) x += base[w * wstride + g * kHeadDim + d0 + e] * f[w];
-            o[e] = static_cast<half_t>(x / l_safe);
+    }
+
+    if constexpr (kFused) {
+        // Last workgroup of this KV head merges its splits.  Every partial is
+        // complete at the coherence point (sc1 stores, vmcnt(0)) before this
+        // workgroup's counter increment; the merging workgroup reads them with
+        // sc1 loads after its own increment returned the final count.
+        __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
+        lds_barrier();
+        if (tid == 0) {
+            const uint32_t prev = __hip_atomic_fetch_add(&a.counters[kvh * kDecCounterStride], 1u, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t flag = 0;
+            if (prev + 1 == static_cast<uint32_t>(a.num_splits)) {
+                flag = 1;
+                // This head is complete: reset its counter for the next launch
+                // and count it towards the position advance (the RMW's latency
+                // overlaps the merge below).
+                __hip_atomic_store(&a.counters[kvh * kDecCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint32_t heads = __hip_atomic_fetch_add(&a.counters[a.num_kv_heads * kDecCounterStride], 1u,
+                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (heads + 1 == static_cast<uint32_t>(a.num_kv_heads)) {
+                    __hip_atomic_store(&a.counters[a.num_kv_heads * kDecCounterStride], 0u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    // Every workgroup has read the position by now.
+                    if (a.advance_position)
+                        __hip_atomic_store(a.position_w, pos_raw + 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            s_flag = flag;
         }
-        const int64_t row = (static_cast<int64_t>(kvh) * a.num_splits + split) * a.group + g;
-        store_half8(a.att_partial + row * kHeadDim + d0, o);
-        if (d0 == 0) a.lse_partial[row] = M + log2f(l_safe);
+        lds_barrier();
+        if (s_flag == 0) return;
+
+        // Merge of this KV head: O[g] = sum_s w_s O_s[g], w_s = 2^(lse_s - M)/sum.
+        // Thread t owns head g = (t/16) % G, 16-byte dim chunk j = t % 16 and the
+        // splits s = sg, sg+SG, ... (sg = (t/16)/G, SG = 16/G); all of its LSE
+        // and partial loads go out together (one memory round trip per batch of
+        // kMergeBatch splits), and max, sum and the split groups are reduced
+        // through LDS.
+        constexpr int kMergeBatch = 16;
+        const int NS = a.num_splits;
+        const int SG = 16 / G;
+        const int g = (tid >> 4) % G, j = tid & 15, sg = (tid >> 4) / G;
+        const bool active = sg < SG;
+        const float* lse = a.lse_partial + static_cast<int64_t>(kvh) * NS * G;
+        const uint16_t* src = a.att_partial + (static_cast<int64_t>(kvh) * NS * G + g) * kHeadDim + 8 * j;
+        float* red_m = reinterpret_cast<float*>(lds);  // [16][16] per (sg, g) max
+        float* red_s = red_m + 256;                    // [16][16] per (sg, g) sum
+        float* part = red_s + 256;                     // [16][16][128] per (sg, g) partial O
+        // Each thread keeps an online (max, sum, acc) over its splits; the
+        // split groups are rescaled to the head's max when combined.
+        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float m_loc = -INFINITY, s_loc = 0.0f;
+        for (int s0 = sg; active && s0 < NS; s0 += kMergeBatch * SG) {
+            half8_t x[kMergeBatch];
+            float lv[kMergeBatch];
+#pragma unroll
+            for (int u = 0; u < kMergeBatch; ++u) {
+                const int s2 = s0 + u * SG;
+                lv[u] = -INFINITY;
+                if (s2 < NS) {
+                    x[u] = load16_agent(src + static_cast<int64_t>(s2) * G * kHeadDim);
+                    lv[u] = __hip_atomic_load(lse + s2 * G + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            float mb = m_loc;
+#pragma unroll
+            for (int u = 0; u < kMergeBatch; ++u) mb = fmaxf(mb, lv[u]);
+            const float r = (m_loc == -INFINITY) ? 0.0f : exp2f(m_loc - mb);
+            s_loc *= r;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] *= r;
+            m_loc = mb;
+#pragma unroll
+            for (int u = 0; u < kMergeBatch; ++u) {
+                if (s0 + u * SG < NS) {
+                    const float w = exp2f(lv[u] - m_loc);
+                    s_loc += w;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[e] += static_cast<float>(x[u][e]) * w;
+                }
+            }
+        }
+        if (active) {
+            if (j == 0) {
+                red_m[sg * 16 + g] = m_loc;
+                red_s[sg * 16 + g] = s_loc;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part[(sg * 16 + g) * kHeadDim + 8 * j + e] = o[e];
+        }
+        lds_barrier();
+        if (tid < G * 16) {
+            const int gg = tid >> 4, jj = tid & 15;
+            float M = -INFINITY;
+            for (int q2 = 0; q2 < SG; ++q2) M = fmaxf(M, red_m[q2 * 16 + gg]);
+            float sum = 0.0f, f[16];
+            for (int q2 = 0; q2 < SG; ++q2) {
+                const float mq = red_m[q2 * 16 + gg];
+                f[q2] = (mq == -INFINITY) ? 0.0f : exp2f(mq - M);
+                sum += red_s[q2 * 16 + gg] * f[q2];
+            }
+            const float inv = 1.0f / fmaxf(sum, 1.0e-8f);
+            half8_t ho;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float x = 0.0f;
+                for (int q2 = 0; q2 < SG; ++q2) x += part[(q2 * 16 + gg) * kHeadDim + 8 * jj + e] * f[q2];
+                ho[e] = static_cast<half_t>(x * inv);
+            }
+            store_half8(a.out + (static_cast<int64_t>(kvh) * G + gg) * kHeadDim + 8 * jj, ho);
+        }
     }
 }
 
-// One wavefront per (head, kv_head): weights from the split LSEs, then each
-// lane accumulates two output dims over the splits.
+// Standalone merge: one workgroup of 64 lanes per (head, kv_head); split
+// weights are staged in LDS, then each lane accumulates two output dims.
 __global__ __launch_bounds__(kWave) void attn_decode_merge_kernel(
     const uint16_t* __restrict__ att, const float* __restrict__ lse, uint16_t* __restrict__ out,
     int group, int num_splits) {
+    __shared__ float w_lds[GROUT_MAX_DECODE_SPLITS];
     const int g = blockIdx.x;
     const int kvh = blockIdx.y;
     const int lane = threadIdx.x;
@@ -239,23 +646,25 @@ __global__ __launch_bounds__(kWave) void attn_decode_merge_kernel(
 
     float mx = -INFINITY;
     for (int s = lane; s < num_splits; s += kWave) mx = fmaxf(mx, L[s * group + g]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = wave_max(mx);
     float sum = 0.0f;
-    for (int s = lane; s < num_splits; s += kWave) sum += exp2f(L[s * group + g] - mx);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    for (int s = lane; s < num_splits; s += kWave) {
+        const float e = exp2f(L[s * group + g] - mx);
+        w_lds[s] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
     const float safe = fmaxf(sum, 1.0e-8f);
+    __syncthreads();
 
     float acc0 = 0.0f, acc1 = 0.0f;
     const uint16_t* base = att + (static_cast<int64_t>(kvh) * num_splits * group + g) * kHeadDim + 2 * lane;
+#pragma unroll 8
     for (int s = 0; s < num_splits; ++s) {
-        const float w = exp2f(L[s * group + g] - mx) / safe;
+        const float w = w_lds[s] / safe;
         const uint32_t pair = *reinterpret_cast<const uint32_t*>(base + static_cast<int64_t>(s) * group * kHeadDim);
-        const half_t h0 = __builtin_bit_cast(half_t, static_cast<uint16_t>(pair & 0xffffu));
-        const half_t h1 = __builtin_bit_cast(half_t, static_cast<uint16_t>(pair >> 16));
-        acc0 += static_cast<float>(h0) * w;
-        acc1 += static_cast<float>(h1) * w;
+        acc0 += static_cast<float>(__builtin_bit_cast(half_t, static_cast<uint16_t>(pair & 0xffffu))) * w;
+        acc1 += static_cast<float>(__builtin_bit_cast(half_t, static_cast<uint16_t>(pair >> 16))) * w;
     }
     const uint16_t o0 = __builtin_bit_cast(uint16_t, static_cast<half_t>(acc0));
     const uint16_t o1 = __builtin_bit_cast(uint16_t, static_cast<half_t>(acc1));
@@ -287,14 +696,11 @@ static float f16_bits_to_f32(uint16_t h) {
 
 using namespace grout;
 
-extern "C" int32_t grout_attn_decode_split(const uint16_t* q, const uint16_t* k_cache,
-                                           const uint16_t* v_cache, uint16_t* att_partial,
-                                           float* lse_partial, uint16_t qk_scale_f16,
-                                           const uint32_t* d_position, int32_t num_kv_heads,
-                                           int32_t group, int32_t head_dim, int32_t max_seq_len,
-                                           int32_t block_n, int32_t num_splits,
-                                           grout_stream_t stream) {
-    GROUT_REQUIRE_PTR(q);
+static int32_t check_attention_args(const uint16_t* k_cache, const uint16_t* v_cache,
+                                    const uint16_t* att_partial, const float* lse_partial,
+                                    const uint32_t* d_position, int32_t num_kv_heads,
+                                    int32_t group, int32_t head_dim, int32_t max_seq_len,
+                                    int32_t block_n, int32_t num_splits, uint16_t qk_scale_f16) {
     GROUT_REQUIRE_PTR(k_cache);
     GROUT_REQUIRE_PTR(v_cache);
     GROUT_REQUIRE_PTR(att_partial);
@@ -309,8 +715,22 @@ extern "C" int32_t grout_attn_decode_split(const uint16_t* q, const uint16_t* k_
     GROUT_REQUIRE(num_splits >= 1 && num_splits <= GROUT_MAX_DECODE_SPLITS, GROUT_ERR_SPLITS);
     const float scale = f16_bits_to_f32(qk_scale_f16);
     GROUT_REQUIRE(scale > 0.0f && scale < 65536.0f, GROUT_ERR_ARG);
+    return GROUT_OK;
+}
 
-    DecodeSplitArgs a;
+extern "C" int32_t grout_attn_decode_split(const uint16_t* q, const uint16_t* k_cache,
+                                           const uint16_t* v_cache, uint16_t* att_partial,
+                                           float* lse_partial, uint16_t qk_scale_f16,
+                                           const uint32_t* d_position, int32_t num_kv_heads,
+                                           int32_t group, int32_t head_dim, int32_t max_seq_len,
+                                           int32_t block_n, int32_t num_splits,
+                                           grout_stream_t stream) {
+    GROUT_REQUIRE_PTR(q);
+    const int32_t st = check_attention_args(k_cache, v_cache, att_partial, lse_partial, d_position,
+                                            num_kv_heads, group, head_dim, max_seq_len, block_n,
+                                            num_splits, qk_scale_f16);
+    if (st != GROUT_OK) return st;
+    DecodeArgs a = {};
     a.q = q;
     a.k_cache = k_cache;
     a.v_cache = v_cache;
@@ -318,12 +738,66 @@ extern "C" int32_t grout_attn_decode_split(const uint16_t* q, const uint16_t* k_
     a.lse_partial = lse_partial;
     a.d_position = d_position;
     // src/kernels.rs:2618-2622: qk_scale_f32 / ln(2), both f32.
-    a.scale_log2 = scale / logf(2.0f);
+    a.scale_log2 = f16_bits_to_f32(qk_scale_f16) / logf(2.0f);
     a.group = group;
+    a.num_kv_heads = num_kv_heads;
     a.max_seq_len = max_seq_len;
     a.block_n = block_n;
     a.num_splits = num_splits;
-    hipLaunchKernelGGL(attn_decode_split_kernel, dim3(num_splits, num_kv_heads), dim3(kDecThreads),
+    hipLaunchKernelGGL(attn_decode_kernel<false>, dim3(num_splits, num_kv_heads), dim3(kDecThreads),
+                       0, to_hip(stream), a);
+    return launch_status();
+}
+
+extern "C" int32_t grout_attn_decode_fused(
+    const uint16_t* qkv, const uint16_t* q_weight, const uint16_t* k_weight,
+    const float* inv_freq, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+    uint16_t* att_partial, float* lse_partial, uint16_t* out, uint32_t* counters,
+    uint32_t* d_position, float eps, uint16_t qk_scale_f16, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len, int32_t block_n,
+    int32_t num_splits, int32_t advance_position, grout_stream_t stream) {
+    GROUT_REQUIRE_PTR(qkv);
+    GROUT_REQUIRE_PTR(q_weight);
+    GROUT_REQUIRE_PTR(k_weight);
+    GROUT_REQUIRE_PTR(inv_freq);
+    GROUT_REQUIRE_PTR(q_out);
+    GROUT_REQUIRE_PTR(out);
+    GROUT_REQUIRE(counters != nullptr, GROUT_ERR_NULL_POINTER);
+    GROUT_REQUIRE((reinterpret_cast<uintptr_t>(counters) & 3u) == 0, GROUT_ERR_ALIGNMENT);
+    GROUT_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
+                  GROUT_ERR_HEADS);
+    GROUT_REQUIRE(eps >= 0.0f && eps < 1.0e30f, GROUT_ERR_ARG);
+    const int32_t group = num_q_heads / num_kv_heads;
+    const int32_t st = check_attention_args(k_cache, v_cache, att_partial, lse_partial, d_position,
+                                            num_kv_heads, group, head_dim, max_seq_len, block_n,
+                                            num_splits, qk_scale_f16);
+    if (st != GROUT_OK) return st;
+    DecodeArgs a = {};
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.att_partial = att_partial;
+    a.lse_partial = lse_partial;
+    a.d_position = d_position;
+    a.scale_log2 = f16_bits_to_f32(qk_scale_f16) / logf(2.0f);
+    a.group = group;
+    a.num_kv_heads = num_kv_heads;
+    a.max_seq_len = max_seq_len;
+    a.block_n = block_n;
+    a.num_splits = num_splits;
+    a.qkv = qkv;
+    a.q_weight = q_weight;
+    a.k_weight = k_weight;
+    a.inv_freq = inv_freq;
+    a.q_out = q_out;
+    a.k_cache_w = k_cache;
+    a.v_cache_w = v_cache;
+    a.out = out;
+    a.counters = counters;
+    a.position_w = d_position;
+    a.eps = eps;
+    a.num_q_heads = num_q_heads;
+    a.advance_position = advance_position != 0;
+    hipLaunchKernelGGL(attn_decode_kernel<true>, dim3(num_splits, num_kv_heads), dim3(kDecThreads),
                        0, to_hip(stream), a);
     return launch_status();
 }
@@ -356,16 +830,22 @@ extern "C" int64_t grout_attn_decode_lse_bytes(int32_t num_kv_heads, int32_t gro
     return static_cast<int64_t>(num_kv_heads) * num_splits * group * 4;
 }
 
+extern "C" int64_t grout_attn_decode_counter_bytes(int32_t num_kv_heads) {
+    if (num_kv_heads <= 0) return GROUT_ERR_ARG;
+    return static_cast<int64_t>(num_kv_heads + 1) * kDecCounterStride * 4;
+}
+
 extern "C" int32_t grout_attn_decode_pick_splits(int32_t cu_count, int32_t num_kv_heads,
                                                  int32_t max_context, int32_t block_n) {
     if (cu_count <= 0) cu_count = 256;
     if (num_kv_heads <= 0 || block_n <= 0 || max_context <= 0) return 1;
-    // Two resident workgroups per CU keep ~64 KB of K/V loads in flight per CU;
-    // a split shorter than 8 tiles spends more on its prologue and the merge
-    // than it saves.
+    // One workgroup per CU (each holds ~130 KB of LDS stages) streaming at the
+    // longest context; a split shorter than one 128-token chunk spends more on
+    // its prologue and the merge than it saves.
     const int64_t tiles = (static_cast<int64_t>(max_context) + block_n - 1) / block_n;
-    int64_t want = (2 * static_cast<int64_t>(cu_count) + num_kv_heads - 1) / num_kv_heads;
-    const int64_t cap = (tiles + 7) / 8;
+    const int64_t min_tiles = (kDecChunk + block_n - 1) / block_n;
+    int64_t want = (static_cast<int64_t>(cu_count) + num_kv_heads - 1) / num_kv_heads;
+    const int64_t cap = (tiles + min_tiles - 1) / min_tiles;
     if (want > cap) want = cap;
     if (want < 1) want = 1;
     if (want > GROUT_MAX_DECODE_SPLITS) want = GROUT_MAX_DECODE_SPLITS;

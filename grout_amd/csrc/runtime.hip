@@ -30,6 +30,7 @@ struct grout_decode_runner {
     grout_decode_layer layer;
     hipStream_t stream = nullptr;
     grout_graph* graph = nullptr;
+    uint32_t next_position = 0;  // device position left by the previous step
 };
 
 extern "C" const char* grout_status_string(int32_t status) {
@@ -125,22 +126,14 @@ extern "C" int32_t grout_graph_destroy(grout_graph* graph) {
     return e2 == hipSuccess ? GROUT_OK : static_cast<int32_t>(e2);
 }
 
-// The three ops of one decode layer, in graph order (src/model.rs:3194-3221,
-// :3428-3473).
-static int32_t record_decode_ops(const grout_decode_layer& L, hipStream_t s) {
-    grout_stream_t gs = reinterpret_cast<grout_stream_t>(s);
-    const int32_t group = L.num_q_heads / L.num_kv_heads;
-    int32_t st = grout_qk_norm_rope_kv_decode(L.qkv, L.q_weight, L.k_weight, L.inv_freq, L.q_out,
-                                              L.k_cache, L.v_cache, L.d_position, L.eps,
-                                              L.num_q_heads, L.num_kv_heads, L.head_dim,
-                                              L.max_seq_len, gs);
-    if (st != GROUT_OK) return st;
-    st = grout_attn_decode_split(L.q_out, L.k_cache, L.v_cache, L.att_partial, L.lse_partial,
-                                 L.qk_scale_f16, L.d_position, L.num_kv_heads, group, L.head_dim,
-                                 L.max_seq_len, L.block_n, L.num_splits, gs);
-    if (st != GROUT_OK) return st;
-    return grout_attn_decode_merge(L.att_partial, L.lse_partial, L.attn_out, L.num_kv_heads, group,
-                                   L.head_dim, L.num_splits, gs);
+// The decode step of one layer: the fused norm/RoPE/KV write + split + merge
+// (src/model.rs:3194-3221, :3428-3473 in one launch), advancing the position.
+static int32_t record_decode_step(const grout_decode_layer& L, hipStream_t s) {
+    return grout_attn_decode_fused(L.qkv, L.q_weight, L.k_weight, L.inv_freq, L.q_out, L.k_cache,
+                                   L.v_cache, L.att_partial, L.lse_partial, L.attn_out, L.counters,
+                                   L.d_position, L.eps, L.qk_scale_f16, L.num_q_heads,
+                                   L.num_kv_heads, L.head_dim, L.max_seq_len, L.block_n,
+                                   L.num_splits, 1, reinterpret_cast<grout_stream_t>(s));
 }
 
 extern "C" int32_t grout_decode_runner_create(const grout_decode_layer* layer,
@@ -151,6 +144,7 @@ extern "C" int32_t grout_decode_runner_create(const grout_decode_layer* layer,
     *runner = nullptr;
     const grout_decode_layer& L = *layer;
     GROUT_REQUIRE_PTR(L.attn_out);
+    GROUT_REQUIRE(L.counters != nullptr, GROUT_ERR_NULL_POINTER);
     GROUT_REQUIRE(L.num_q_heads > 0 && L.num_kv_heads > 0 && L.num_q_heads % L.num_kv_heads == 0,
                   GROUT_ERR_HEADS);
     GROUT_REQUIRE(prime_position < static_cast<uint32_t>(L.max_seq_len > 0 ? L.max_seq_len : 0),
@@ -160,14 +154,14 @@ extern "C" int32_t grout_decode_runner_create(const grout_decode_layer* layer,
     // outside capture (src/model.rs:2561-3115).
     int32_t st = grout_set_position_async(L.d_position, prime_position, stream);
     if (st != GROUT_OK) return st;
-    st = record_decode_ops(L, s);
+    st = record_decode_step(L, s);
     if (st != GROUT_OK) return st;
     hipError_t e = hipStreamSynchronize(s);
     if (e != hipSuccess) return static_cast<int32_t>(e);
 
     st = grout_graph_begin(stream);
     if (st != GROUT_OK) return st;
-    int32_t rec = record_decode_ops(L, s);
+    int32_t rec = record_decode_step(L, s);
     grout_graph* g = nullptr;
     st = grout_graph_end(stream, &g);
     if (rec != GROUT_OK) {
@@ -183,6 +177,7 @@ extern "C" int32_t grout_decode_runner_create(const grout_decode_layer* layer,
     r->layer = L;
     r->stream = s;
     r->graph = g;
+    r->next_position = prime_position + 1;  // the prime pass advanced it
     *runner = r;
     return GROUT_OK;
 }
@@ -193,9 +188,13 @@ extern "C" int32_t grout_decode_runner_step(grout_decode_runner* runner, uint32_
     // engine's max_seq_len.
     GROUT_REQUIRE(position < static_cast<uint32_t>(runner->layer.max_seq_len), GROUT_ERR_SEQ_RANGE);
     grout_stream_t gs = reinterpret_cast<grout_stream_t>(runner->stream);
-    int32_t st = grout_set_position_async(runner->layer.d_position, position, gs);
-    if (st != GROUT_OK) return st;
-    return grout_graph_launch(runner->graph, gs);
+    if (position != runner->next_position) {
+        const int32_t st = grout_set_position_async(runner->layer.d_position, position, gs);
+        if (st != GROUT_OK) return st;
+    }
+    const int32_t st = grout_graph_launch(runner->graph, gs);
+    if (st == GROUT_OK) runner->next_position = position + 1;
+    return st;
 }
 
 extern "C" int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner) {

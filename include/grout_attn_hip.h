@@ -152,6 +152,31 @@ int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_pa
                                 uint16_t* out, int32_t num_kv_heads, int32_t group,
                                 int32_t head_dim, int32_t num_splits, grout_stream_t stream);
 
+/* --------------------------------------- fused decode step (A3+A9+A10) */
+/* One launch doing what grout's decode graph records as three ops per layer
+ * (src/model.rs:3194-3221, 3428-3473): RMSNorm + RoPE of the G query rows of
+ * each KV head (q_out rows [0, num_q_heads) are written, as A3 does), the
+ * K/V-cache write at *d_position, split-K GQA attention over s_kv =
+ * *d_position + 1 keys into att_partial/lse_partial (same layout and split
+ * boundaries as grout_attn_decode_split) and the LSE merge into out
+ * [num_kv_heads, group, 128].  The last workgroup of each KV head merges (an
+ * agent-scope acq_rel counter in `counters`).
+ *   counters: grout_attn_decode_counter_bytes(num_kv_heads) bytes, zero
+ *   before the first call; every call leaves them zero again.
+ *   advance_position != 0: the launch ends by storing *d_position + 1, so a
+ *   graph replayed once per token needs no position write in between.
+ * Calls that overlap on one set of counters race. */
+int32_t grout_attn_decode_fused(const uint16_t* qkv, const uint16_t* q_weight,
+                                const uint16_t* k_weight, const float* inv_freq,
+                                uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                uint16_t* att_partial, float* lse_partial, uint16_t* out,
+                                uint32_t* counters, uint32_t* d_position, float eps,
+                                uint16_t qk_scale_f16, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                                int32_t block_n, int32_t num_splits, int32_t advance_position,
+                                grout_stream_t stream);
+int64_t grout_attn_decode_counter_bytes(int32_t num_kv_heads);
+
 /* Bytes of att_partial (f16) and lse_partial (f32) for a split count, as
  * allocated at src/model.rs:2508-2525.  Returns < 0 on invalid arguments. */
 int64_t grout_attn_decode_partial_bytes(int32_t num_kv_heads, int32_t group, int32_t head_dim,
@@ -187,9 +212,12 @@ int32_t grout_set_position_async(uint32_t* d_position, uint32_t position,
 
 /* ------------------------------------------- decode graph runner (A14) */
 /* The attention slice of DecodeCudaGraphRunner (src/model.rs:318-493): one
- * hipGraph holding {fused QK norm/RoPE/KV write, split-K decode, merge} for
- * one layer's buffers, replayed per token with only the device position
- * updated.  All pointers are borrowed and must outlive the runner. */
+ * hipGraph holding the fused decode step (grout_attn_decode_fused: QK
+ * norm/RoPE/KV write, split-K decode, merge) for one layer's buffers,
+ * replayed per token.  The graph advances the device position itself; a step
+ * writes the position (stream-ordered) only when it is not the one the
+ * previous step left.  All pointers are borrowed and must outlive the runner,
+ * which owns *d_position and the counters while it lives. */
 typedef struct grout_decode_layer {
     const uint16_t* qkv;       /* [(Hq + 2*Hkv) * 128] f16 QKV GEMV output */
     const uint16_t* q_weight;  /* [128] f16 */
@@ -202,6 +230,7 @@ typedef struct grout_decode_layer {
     float* lse_partial;        /* grout_attn_decode_lse_bytes */
     uint16_t* attn_out;        /* [Hkv, G, 128] f16 */
     uint32_t* d_position;      /* device u32 */
+    uint32_t* counters;        /* grout_attn_decode_counter_bytes, zeroed */
     float eps;
     uint16_t qk_scale_f16;
     int32_t num_q_heads;
@@ -213,11 +242,13 @@ typedef struct grout_decode_layer {
 } grout_decode_layer;
 
 typedef struct grout_decode_runner grout_decode_runner;
-/* Validates, runs the three ops once eagerly (the prime pass of
- * src/model.rs:2561-3115) at `prime_position`, then captures them. */
+/* Validates, runs the step once eagerly (the prime pass of
+ * src/model.rs:2561-3115) at `prime_position`, then captures it. */
 int32_t grout_decode_runner_create(const grout_decode_layer* layer, uint32_t prime_position,
                                    grout_stream_t stream, grout_decode_runner** runner);
-/* launch_step: write the position (stream-ordered), replay the graph.  No host sync. */
+/* launch_step (src/model.rs:363-403): make the device position `position`
+ * (a stream-ordered write unless the previous step already left it there),
+ * replay the graph.  No host sync. */
 int32_t grout_decode_runner_step(grout_decode_runner* runner, uint32_t position);
 /* zero_kv_caches (src/model.rs:433-462): clear both caches in place; pointers
  * stay valid for the captured graph.  Synchronises the runner's stream. */

@@ -127,8 +127,9 @@ def test_decode_equals_prefill_last_row(gpu):
 
 
 def test_graph_runner_replay(gpu):
-    """DecodeGraphRunner: capture once, replay at successive positions; each replay
-    equals the eager ops and the oracle (norm/RoPE/KV write + split + merge)."""
+    """DecodeGraphRunner: capture once, replay at successive positions (the graph
+    advances the position itself), then jump to a non-consecutive position; each
+    replay equals the oracle's norm/RoPE/KV write + split + merge."""
     import torch
 
     import grout_amd
@@ -157,8 +158,7 @@ def test_graph_runner_replay(gpu):
         num_q_heads=hq, num_kv_heads=hkv, num_splits=ns, prime_position=p0)
     kc_ref, vc_ref = kc.copy(), vc.copy()
     try:
-        for step in range(5):
-            pos = p0 + step
+        for step, pos in enumerate([p0, p0 + 1, p0 + 2, p0 + 3, p0 + 7, p0 + 8]):
             qkv = normal_f16(g, ((hq + 2 * hkv) * D,))
             with torch.cuda.stream(runner.stream):
                 dev["qkv"].copy_(torch.from_numpy(qkv).cuda())
@@ -173,6 +173,8 @@ def test_graph_runner_replay(gpu):
                                                     pos, BN, ns)
             assert_close_attn(out, oracle.attn_decode_merge(a_ref, l_ref, G), f"replay {step}")
         # The prime pass wrote slot p0 once before capture; the replays rewrote it.
+        assert int(dev["position"].item()) == p0 + 9
+        assert int(runner.counters.abs().sum().item()) == 0
         kc_dev = dev["k_cache"].cpu().numpy()
         from tests._util import f16_ulp_diff
         assert f16_ulp_diff(kc_dev, kc_ref).max() <= 1
@@ -180,3 +182,110 @@ def test_graph_runner_replay(gpu):
         assert int(dev["k_cache"].abs().sum().item()) == 0
     finally:
         runner.close()
+
+
+def _fused_case(seed, hq, hkv, MS):
+    from tests._util import norm_weight
+
+    g = rng(seed)
+    qkv = normal_f16(g, ((hq + 2 * hkv) * D,))
+    qw, kw = norm_weight(g), norm_weight(g)
+    kc = normal_f16(g, (hkv, MS, D))
+    vc = normal_f16(g, (hkv, MS, D))
+    return g, qkv, qw, kw, kc, vc
+
+
+@pytest.mark.parametrize("hq,hkv,pos,MS,ns,seed", [
+    (32, 8, 4096, 4200, 16, 70),   # config c2 shapes
+    (32, 8, 4096, 4200, 33, 71),   # split count not dividing the tiles
+    (64, 8, 2047, 2048, 32, 72),   # G = 8, last cache slot
+    (4, 2, 0, 8, 4, 73),           # s_kv = 1, empty splits
+    (16, 16, 300, 512, 3, 74),     # G = 1
+])
+def test_fused_step_matches_oracle(gpu, hq, hkv, pos, MS, ns, seed):
+    """grout_attn_decode_fused = norm/RoPE/KV write + split + merge of the oracle;
+    counters return to zero; the position advances only when asked."""
+    import torch
+
+    import grout_amd
+    from tests._util import EPS, THETA, f16_ulp_diff
+
+    _, qkv, qw, kw, kc, vc = _fused_case(seed, hq, hkv, MS)
+    G = hq // hkv
+    inv = oracle.build_inv_freq(THETA)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    dkc, dvc = t(kc), t(vc)
+    q_out = torch.full(((hq + hkv), D), 2.5, dtype=torch.float16, device="cuda")
+    out = torch.zeros((hkv, G, D), dtype=torch.float16, device="cuda")
+    att, lse = grout_amd.decode_scratch(hkv, G, ns)
+    counters = grout_amd.decode_counters(hkv)
+    dpos = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    for advance in (False, True):
+        grout_amd.decode_fused(t(qkv), t(qw), t(kw), t(inv), q_out, dkc, dvc, att, lse, out,
+                               counters, dpos, EPS, qk_scale_f16_bits(), hq, hkv,
+                               advance_position=advance)
+        torch.cuda.synchronize()
+        assert int(dpos.item()) == pos + (1 if advance else 0)
+        assert int(counters.abs().sum().item()) == 0, "counters not reset"
+        dpos.fill_(pos)
+
+    qo_ref = np.full(((hq + hkv), D), np.float16(2.5), dtype=np.float16)
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    oracle.qk_norm_rope_kv_decode(qkv, qw, kw, inv, qo_ref, kc_ref, vc_ref, pos, EPS, hq, hkv)
+    qo = q_out.cpu().numpy()
+    assert f16_ulp_diff(qo[:hq], qo_ref[:hq]).max() <= 1
+    assert np.array_equal(qo[hq:].view(np.uint16), qo_ref[hq:].view(np.uint16))
+    kc_dev, vc_dev = dkc.cpu().numpy(), dvc.cpu().numpy()
+    assert np.array_equal(vc_dev.view(np.uint16), vc_ref.view(np.uint16))
+    assert f16_ulp_diff(kc_dev, kc_ref).max() <= 1
+    qg = np.ascontiguousarray(qo_ref[:hq].reshape(hkv, G, D))
+    a_ref, l_ref = oracle.attn_decode_split(qg, kc_ref, vc_ref, qk_scale_f16_bits(), pos, BN, ns)
+    s_kv = pos + 1
+    nonempty = np.array([oracle.decode_split_range(s_kv, BN, ns, s)[0]
+                         < oracle.decode_split_range(s_kv, BN, ns, s)[1] for s in range(ns)])
+    rows = np.repeat(nonempty, G)
+    a_dev, l_dev = att.cpu().numpy(), lse.cpu().numpy()
+    assert_close_attn(a_dev[:, rows], a_ref[:, rows], "fused att_partial")
+    assert np.max(np.abs(l_dev[:, rows] - l_ref[:, rows])) < 1e-3
+    out_ref = oracle.attn_decode_merge(a_ref, l_ref, G)
+    assert_close_attn(out.cpu().numpy(), out_ref, "fused out vs oracle")
+    assert_close_attn(out.cpu().numpy(), _fp32_decode(qg, kc_ref, vc_ref, pos),
+                      "fused out vs fp32 decode")
+
+
+def test_fused_consecutive_steps_advance(gpu):
+    """Ten launches with advance_position walk the cache forward one slot each,
+    with no host write of the position in between."""
+    import torch
+
+    import grout_amd
+    from tests._util import EPS, THETA
+
+    hq, hkv, MS, p0, ns = 32, 8, 300, 250, 8
+    g, _, qw, kw, kc, vc = _fused_case(75, hq, hkv, MS)
+    G = hq // hkv
+    inv = oracle.build_inv_freq(THETA)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    dkc, dvc, dqw, dkw, dinv = t(kc), t(vc), t(qw), t(kw), t(inv)
+    q_out = torch.zeros(((hq + hkv), D), dtype=torch.float16, device="cuda")
+    out = torch.zeros((hkv, G, D), dtype=torch.float16, device="cuda")
+    att, lse = grout_amd.decode_scratch(hkv, G, ns)
+    counters = grout_amd.decode_counters(hkv)
+    dpos = torch.tensor([p0], dtype=torch.int32, device="cuda")
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    dqkv = torch.empty(((hq + 2 * hkv) * D,), dtype=torch.float16, device="cuda")
+    for step in range(10):
+        qkv = normal_f16(g, ((hq + 2 * hkv) * D,))
+        dqkv.copy_(t(qkv))
+        grout_amd.decode_fused(dqkv, dqw, dkw, dinv, q_out, dkc, dvc, att, lse, out, counters,
+                               dpos, EPS, qk_scale_f16_bits(), hq, hkv, advance_position=True)
+        torch.cuda.synchronize()
+        qo_ref = np.zeros(((hq + hkv), D), np.float16)
+        oracle.qk_norm_rope_kv_decode(qkv, qw, kw, inv, qo_ref, kc_ref, vc_ref, p0 + step, EPS,
+                                      hq, hkv)
+        qg = np.ascontiguousarray(qo_ref[:hq].reshape(hkv, G, D))
+        a_ref, l_ref = oracle.attn_decode_split(qg, kc_ref, vc_ref, qk_scale_f16_bits(),
+                                                p0 + step, BN, ns)
+        assert_close_attn(out.cpu().numpy(), oracle.attn_decode_merge(a_ref, l_ref, G),
+                          f"step {step}")
+    assert int(dpos.item()) == p0 + 10
