@@ -36,6 +36,12 @@ if ROOT not in sys.path:
 METRIC = ("prefill attn TFLOP/s (% fp16 MFMA peak); decode attn GB/s (% HBM peak), 1 GPU")
 PEAK_TFLOPS_F16 = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz (dense fp16 MFMA)
 PEAK_HBM_GBS = 8000.0      # HBM3E
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0), the
+# scales read off a 1 GiB copy; the runs and figures are in profiles/*.txt.
+PMC_TRAFFIC_BYTES = {
+    "attn_prefill_c3": (71373.6 * 2.0 + 65732.7) * 1024,
+    "attn_decode_fused_c4": (66019.3 * 2.0 + 2108.5) * 1024,
+}
 D = 128
 EPS = 1e-6
 THETA = 1e6
@@ -227,6 +233,11 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "norm"], default="all",
+                    help="run one workload only (for profiling runs); prints no JSON line")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a plain 1 GiB device-to-device copy (reads and writes 1 GiB) "
+                         "to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings, then exit")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -247,6 +258,29 @@ def main(argv=None) -> int:
 
     def log(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    if args.copy_calibration:
+        src = torch.empty((1 << 30,), dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 1 GiB device copies done")
+        return 0
+    if args.only != "all":
+        if args.only == "prefill":
+            pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
+            log(f"prefill c3: {pre['ms']:.3f} ms/launch, {pre['tflops']:.1f} TFLOP/s")
+        elif args.only == "norm":
+            nrm = bench_norm(torch, ga, args.steps, args.warmup, gen)
+            log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
+        else:
+            dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, args.warmup, gen,
+                               args.steps)
+            log(f"decode c4: graph step {dec['step_us']:.2f} us, fused {dec['fused_us']:.2f} us "
+                f"({dec['fused_gbs']:.0f} GB/s), split {dec['split_us']:.2f} us")
+        return 0
 
     log("prefill c3 ...")
     pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
@@ -295,7 +329,8 @@ def main(argv=None) -> int:
                                "32 Q / 8 KV heads, head_dim 128, f16 (fp32 accumulation)",
                    "seq_len": pre["S"], "num_q_heads": pre["hq"], "num_kv_heads": pre["hkv"],
                    "head_dim": D, "flops_per_step": pre["flops"]},
-        "roofline": rl("mfma", pre["tflops"], PEAK_TFLOPS_F16, "TFLOP/s"),
+        "roofline": rl("mfma", pre["tflops"], PEAK_TFLOPS_F16, "TFLOP/s",
+                       traffic=round(PMC_TRAFFIC_BYTES["attn_prefill_c3"])),
         "cpu_baseline": cpu,
         "decode": {
             "workload": "c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context 32768, "
@@ -306,7 +341,8 @@ def main(argv=None) -> int:
             "fused_kernel_us": round(dec["fused_us"], 3),
             "standalone_split_us": round(dec["split_us"], 3),
             "standalone_merge_us": round(dec["merge_us"], 3),
-            "roofline": rl("hbm", dec["fused_gbs"], PEAK_HBM_GBS, "GB/s"),
+            "roofline": rl("hbm", dec["fused_gbs"], PEAK_HBM_GBS, "GB/s",
+                           traffic=round(PMC_TRAFFIC_BYTES["attn_decode_fused_c4"])),
             "step_frac_of_hbm_peak": round(dec["step_gbs"] / PEAK_HBM_GBS, 4),
             "cpu_baseline": cpu_dec,
         },

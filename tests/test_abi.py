@@ -1,0 +1,208 @@
+"""CPU tests of the C-ABI boundary (no GPU, no kernel launches).
+
+* the library loads and exports every function include/grout_attn_hip.h declares;
+* each argument check returns its documented status before any HIP call, as the
+  reference's ensure!s do before a launch (src/model.rs:4480-4560, 5564-5637);
+* host-side helpers (RoPE table, split picking, scratch sizes) behave as specified;
+* the Python mirror raises the reference's ensure! messages on bad shapes.
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "grout_attn_hip.h")
+
+# Fake device addresses: never dereferenced, the checks reject the call first.
+A = 0x100000        # 16-byte aligned
+U = 0x100002        # misaligned
+
+
+@pytest.fixture(scope="module")
+def L():
+    import grout_amd
+
+    return grout_amd.lib()
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(grout_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(L):
+    import grout_amd._lib as gl
+
+    names = header_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(L, name), f"{name} declared in the header but not exported"
+        assert name in gl.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_status_strings(L):
+    import grout_amd._lib as gl
+
+    for code, name in gl.STATUS_NAMES.items():
+        text = L.grout_status_string(code).decode()
+        assert text and text != "unknown status", name
+    assert L.grout_status_string(-999).decode() == "unknown status"
+
+
+S = None  # null stream
+
+
+def prefill_norm(L, **kw):
+    args = dict(q=A, k=A, v=A, qw=A, kw=A, inv=A, qo=A, kc=A, vc=A, eps=1e-6, ps=0, S=4,
+                hq=4, hkv=2, D=128, MS=16)
+    args.update(kw)
+    return L.grout_qk_norm_rope_kv_prefill(
+        args["q"], args["k"], args["v"], args["qw"], args["kw"], args["inv"], args["qo"],
+        args["kc"], args["vc"], args["eps"], args["ps"], args["S"], args["hq"], args["hkv"],
+        args["D"], args["MS"], S)
+
+
+def test_norm_prefill_checks(L):
+    assert prefill_norm(L, q=0) == -1
+    assert prefill_norm(L, vc=0) == -1
+    assert prefill_norm(L, k=U) == -2
+    assert prefill_norm(L, D=64) == -3
+    assert prefill_norm(L, hq=3, hkv=2) == -4
+    assert prefill_norm(L, hkv=0) == -4
+    assert prefill_norm(L, ps=13, S=4, MS=16) == -5      # 17 > max_seq_len
+    assert prefill_norm(L, S=-1) == -5
+    assert prefill_norm(L, eps=-1.0) == -9
+    assert prefill_norm(L, eps=float("nan")) == -9
+    assert prefill_norm(L, S=0) == 0                      # empty: nothing launched
+
+
+def test_norm_decode_checks(L):
+    f = L.grout_qk_norm_rope_kv_decode
+    assert f(A, A, A, A, A, A, A, 0, 1e-6, 4, 2, 128, 16, S) == -1
+    assert f(A, A, A, A, A, A, A, A + 2, 1e-6, 4, 2, 128, 16, S) == -2
+    assert f(A, A, A, A, A, A, A, A, 1e-6, 4, 2, 96, 16, S) == -3
+    assert f(A, A, A, A, A, A, A, A, 1e-6, 4, 3, 128, 16, S) == -4
+    assert f(A, A, A, A, U, A, A, A, 1e-6, 4, 2, 128, 16, S) == -2
+
+
+def test_prefill_checks(L):
+    f = L.grout_attn_prefill
+    ok = dict(q=A, k=A, v=A, o=A, sc=0.088, hq=4, hkv=2, D=128, ql=8, kv=8, qs=0, MS=16)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return f(a["q"], a["k"], a["v"], a["o"], a["sc"], a["hq"], a["hkv"], a["D"], a["ql"],
+                 a["kv"], a["qs"], a["MS"], S)
+
+    assert call(o=0) == -1
+    assert call(q=U) == -2
+    assert call(D=256) == -3
+    assert call(hq=5) == -4
+    assert call(kv=0) == -6
+    assert call(kv=17) == -6           # kv_len > max_seq_len
+    assert call(qs=-1) == -6
+    assert call(sc=0.0) == -9
+    assert call(ql=0) == 0
+
+
+def test_decode_split_merge_checks(L):
+    sp = L.grout_attn_decode_split
+    # q, k, v, att, lse, scale, pos, hkv, G, D, MS, BN, NKS
+    assert sp(A, A, A, A, A, 0x2DA8, 0, 8, 4, 128, 64, 32, 4, S) == -1
+    assert sp(A, A, A, U, A, 0x2DA8, A, 8, 4, 128, 64, 32, 4, S) == -2
+    assert sp(A, A, A, A, A, 0x2DA8, A, 8, 4, 64, 64, 32, 4, S) == -3
+    assert sp(A, A, A, A, A, 0x2DA8, A, 8, 17, 128, 64, 32, 4, S) == -7
+    assert sp(A, A, A, A, A, 0x2DA8, A, 8, 4, 128, 64, 0, 4, S) == -8
+    assert sp(A, A, A, A, A, 0x2DA8, A, 8, 4, 128, 64, 32, 1025, S) == -8
+    assert sp(A, A, A, A, A, 0x0000, A, 8, 4, 128, 64, 32, 4, S) == -9   # scale 0
+    assert sp(A, A, A, A, A, 0x7C00, A, 8, 4, 128, 64, 32, 4, S) == -9   # scale inf
+    mg = L.grout_attn_decode_merge
+    assert mg(0, A, A, 8, 4, 128, 4, S) == -1
+    assert mg(A, A, A, 8, 0, 128, 4, S) == -7
+    assert mg(A, A, A, 8, 4, 128, 0, S) == -8
+
+
+def test_decode_fused_checks(L):
+    f = L.grout_attn_decode_fused
+    base = [A] * 12 + [1e-6, 0x2DA8, 32, 8, 128, 64, 32, 4, 1, S]
+
+    def call(i, v):
+        a = list(base)
+        a[i] = v
+        return f(*a)
+
+    assert f(*base[:10], 0, *base[11:]) == -1            # counters
+    assert call(0, 0) == -1                               # qkv
+    assert call(11, A + 2) == -2                          # position misaligned
+    assert call(14, 30) == -4                             # heads
+    assert call(16, 64) == -3                             # head_dim
+    assert call(12, -1.0) == -9                           # eps
+
+
+def test_graph_handle_checks(L):
+    assert L.grout_graph_begin(None) == -10
+    assert L.grout_graph_launch(None, None) == -10
+    assert L.grout_graph_destroy(None) == 0
+    assert L.grout_set_position_async(None, 3, None) == -1
+    assert L.grout_decode_runner_step(None, 0) == -10
+    assert L.grout_decode_runner_destroy(None) == 0
+
+
+def test_inv_freq_matches_oracle(L):
+    import ctypes
+
+    for theta in (1e4, 1e6, 5e5):
+        out = (ctypes.c_float * 64)()
+        assert L.grout_build_inv_freq(theta, 128, out) == 0
+        got = np.array(list(out), dtype=np.float32)
+        assert np.array_equal(got, oracle.build_inv_freq(theta))
+    out = (ctypes.c_float * 64)()
+    assert L.grout_build_inv_freq(1e6, 127, out) == -3
+    assert L.grout_build_inv_freq(-1.0, 128, out) == -9
+
+
+def test_scratch_sizes(L):
+    assert L.grout_attn_decode_partial_bytes(8, 8, 128, 32) == 8 * 32 * 8 * 128 * 2
+    assert L.grout_attn_decode_lse_bytes(8, 8, 32) == 8 * 32 * 8 * 4
+    assert L.grout_attn_decode_counter_bytes(8) >= 9 * 4
+    assert L.grout_attn_decode_partial_bytes(0, 8, 128, 32) < 0
+
+
+def test_pick_splits(L):
+    f = L.grout_attn_decode_pick_splits
+    # One workgroup per CU at long context: Hkv * NKS covers the CUs.
+    assert f(256, 8, 32768 + 1024, 32) * 8 >= 256
+    # Short contexts do not get splits shorter than one 64-token chunk.
+    assert f(256, 8, 64, 32) == 1
+    assert f(256, 8, 4097, 32) <= (4097 + 63) // 64
+    assert f(0, 8, 32768, 32) >= 1
+    for ctx in (1, 100, 4097, 33792, 10 ** 6):
+        assert 1 <= f(256, 8, ctx, 32) <= 1024
+
+
+def test_python_mirror_shape_errors():
+    torch = pytest.importorskip("torch")
+    import grout_amd
+
+    h = torch.float16
+    q = torch.zeros((4, 8, 128), dtype=h)
+    k = torch.zeros((4, 2, 128), dtype=h)
+    bad_v = torch.zeros((3, 2, 128), dtype=h)
+    w = torch.ones(128, dtype=h)
+    inv = torch.ones(64)
+    cache = torch.zeros((2, 16, 128), dtype=h)
+    with pytest.raises(grout_amd.GroutError, match="v shape mismatch"):
+        grout_amd.qk_norm_rope_kv_prefill(q, k, bad_v, w, w, inv, torch.zeros_like(q), cache,
+                                          cache, 1e-6, 0)
+    with pytest.raises(grout_amd.GroutError, match="exceeds max_seq_len"):
+        grout_amd.qk_norm_rope_kv_prefill(q, k, k, w, w, inv, torch.zeros_like(q), cache, cache,
+                                          1e-6, 13)
+    with pytest.raises(grout_amd.GroutError, match="attend output shape mismatch"):
+        grout_amd.attend_prefill(q, cache, cache, torch.zeros((4, 4, 128), dtype=h), 0)
+    with pytest.raises(grout_amd.GroutError, match="rank 3"):
+        grout_amd.attend_prefill(q[0], cache, cache, q[0], 0)
