@@ -9,13 +9,13 @@
 //   l = l*alpha + sum(p); acc = acc*alpha + f16(p) V; out = f16(acc/max(l,1e-8)).
 //
 // Shape of the kernel (MI355X-first):
-//  * Workgroup = 4 wavefronts, one per SIMD.  A wavefront owns 64 query rows
-//    of one query head; the 4 wavefronts of a workgroup are query heads of
-//    the same KV head (GQA packing: a K/V tile is fetched once from HBM for
-//    G heads), e.g. G=4: 4 heads x the same 64 positions.
-//  * K/V tiles of 64 keys are staged in LDS, double buffered: the next
-//    tile's global loads are issued before the current tile is computed and
-//    land in the other buffer after it; one workgroup barrier per tile.
+//  * Workgroup = 8 wavefronts, two per SIMD.  A wavefront owns 32 query rows
+//    of one query head; the 8 wavefront tasks of a workgroup belong to the
+//    same KV head (GQA packing: a K/V tile is fetched once from HBM for all
+//    of them), e.g. G=4: 4 heads x the same 64 positions.
+//  * K/V tiles of 64 keys go straight from HBM into LDS (direct-to-LDS DMA,
+//    no register staging) through a 3-stage ring: tile j+2 is issued right
+//    after the barrier that opens tile j; one workgroup barrier per tile.
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_f16 (K rows = A operand, 16-byte LDS
 //    reads; Q^T = B operand held in registers for the whole loop), so each
 //    lane owns one query row and the row softmax needs a single cross-lane

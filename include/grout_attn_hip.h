@@ -159,8 +159,9 @@ int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_pa
  * K/V-cache write at *d_position, split-K GQA attention over s_kv =
  * *d_position + 1 keys into att_partial/lse_partial (same layout and split
  * boundaries as grout_attn_decode_split) and the LSE merge into out
- * [num_kv_heads, group, 128].  The last workgroup of each KV head merges (an
- * agent-scope acq_rel counter in `counters`).
+ * [num_kv_heads, group, 128].  The last workgroup of each KV head merges: it
+ * is found by an agent-scope counter in `counters`, and the partials reach it
+ * through device-coherent stores completed before that counter moves.
  *   counters: grout_attn_decode_counter_bytes(num_kv_heads) bytes, zero
  *   before the first call; every call leaves them zero again.
  *   advance_position != 0: the launch ends by storing *d_position + 1, so a
