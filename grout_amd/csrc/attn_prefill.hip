@@ -13,20 +13,30 @@
 //    of one query head; the 8 wavefront tasks of a workgroup belong to the
 //    same KV head (GQA packing: a K/V tile is fetched once from HBM for all
 //    of them), e.g. G=4: 4 heads x the same 64 positions.
+//  * Ping-pong: waves 0-3 and 4-7 run the same per-tile program one phase
+//    apart.  A tile is a GEMM phase (PV of the previous tile + S of this
+//    tile, 32 MFMAs) and a softmax phase (VALU, v_exp_f32); while one wave of
+//    a SIMD is in its GEMM phase the other is in its softmax, and a workgroup
+//    barrier between phases keeps the two groups in step.
 //  * K/V tiles of 64 keys go straight from HBM into LDS (direct-to-LDS DMA,
-//    no register staging) through a 3-stage ring: tile j+2 is issued right
-//    after the barrier that opens tile j; one workgroup barrier per tile.
+//    no register staging) through a 4-stage ring; tile t+2 is issued in the
+//    phase that first reads tile t.
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_f16 (K rows = A operand, 16-byte LDS
 //    reads; Q^T = B operand held in registers for the whole loop), so each
 //    lane owns one query row and the row softmax needs a single cross-lane
 //    step (v_permlane32_swap).
 //  * O^T += V^T P^T: P^T comes straight from the S^T accumulators (the
 //    reduction slots are ordered to match), V^T from ds_read_b64_tr_b16.
+//    LDS operands are read a few MFMAs ahead into a register ring.
+//  * The running max is raised only when P would leave f16 range, so most
+//    tiles need no row max and no rescale.
 //  * Causal tile skipping per wavefront; masking only on diagonal tiles.
 //  * Heavy (late-position) workgroups launch first (longest-processing-time
 //    order) and all workgroups of one KV head go to one XCD so its K/V stay
 //    in that XCD's L2.
 #include <math.h>
+
+#include <type_traits>
 
 #include "abi_util.h"
 #include "common.h"
@@ -45,12 +55,14 @@ constexpr int kPfVBlock = 1056;
 constexpr int kPfKBytes = 16 * kPfKBlock;
 constexpr int kPfVBytes = 16 * kPfVBlock;
 constexpr int kPfStageBytes = kPfKBytes + kPfVBytes;
-constexpr int kPfStages = 3;
+constexpr int kPfStages = 4;
 constexpr float kPfNegBig = -1.0e30f;
 // Lazy rescale: the running max used for p = 2^(c*s - m) is only raised when
-// a row's max grows by more than this (log2 units), so p <= 2^8 and O is
-// rescaled on few tiles.  The normalised result is the same function.
-constexpr float kPfRescaleSlack = 8.0f;
+// some p of a tile would reach this bound (f16 holds up to 65504), so O is
+// rescaled on few tiles and no per-tile row max is needed otherwise.
+constexpr float kPfPsumLimit = 32768.0f;
+// LDS operand read-ahead of the GEMM phase, in MFMAs.
+constexpr int kPfAhead = 4;
 
 struct PrefillArgs {
     const uint16_t* q;
@@ -91,16 +103,30 @@ __device__ __forceinline__ void lds_dma16(const void* gbase, uint32_t voff, uint
 // maximum, i.e. not waited on).
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
-// NBK: 32-row query blocks per wavefront (rows = 32*NBK); WAVES: wavefronts
-// per workgroup (all on query heads of one KV head).
-template <int NBK, int WAVES>
-__global__ __launch_bounds__(WAVES * kWave, 1) void attn_prefill_kernel(PrefillArgs a) {
-    constexpr int kRows = 32 * NBK;
-    constexpr int kDmaPerWave = 16 / WAVES;  // K blocks (and V blocks) per wavefront
+// Workgroup barrier that also orders LDS: this wavefront's LDS reads have
+// completed (a stage may be refilled right after the barrier) and the
+// compiler moves no memory access across it.
+__device__ __forceinline__ void pf_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Workgroup: 8 wavefronts x 32 query rows, all on query heads of one KV head.
+// Waves 0-3 (group A, one per SIMD) and 4-7 (group B) run the same per-tile
+// program one phase apart ("ping-pong"): a tile is two phases, GEMM (PV of the
+// previous tile + S of this tile, 32 MFMAs) and softmax (VALU + v_exp_f32),
+// and while group A is in one, group B is in the other, so each SIMD always
+// has one wavefront feeding the matrix core while the other does its softmax.
+// A workgroup barrier separates the phases and keeps the two groups in step.
+constexpr int kPfWaves = 8;
+constexpr int kPfRows = 32;
+
+__global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(PrefillArgs a) {
+    constexpr int kDmaPerWave = 16 / kPfWaves;  // K blocks (and V blocks) per wavefront
     __shared__ __attribute__((aligned(1024))) unsigned char pf_lds[kPfStages * kPfStageBytes];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int grp = wave >> 2;  // 0: group A, 1: group B (one phase behind)
     const int lane = tid % kWave;
     const int l32 = lane & 31;
     const int hl = lane >> 5;  // which half of the wavefront
@@ -113,18 +139,18 @@ __global__ __launch_bounds__(WAVES * kWave, 1) void attn_prefill_kernel(PrefillA
     const int T = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
     const int kvh = T / a.blocks_per_head;
     const int rblk = T % a.blocks_per_head;
-    const int u = rblk * WAVES + wave;
+    const int u = rblk * kPfWaves + wave;
     const bool task_ok = u < a.tasks_per_head;
     const int pt = a.n_pos_tiles - 1 - u / a.group;
     const int g = u % a.group;
     const int qh = kvh * a.group + g;
-    const int row0 = pt * kRows;
+    const int row0 = pt * kPfRows;
     const int pos0 = a.query_start + row0;
 
-    const int pt_max = a.n_pos_tiles - 1 - (rblk * WAVES) / a.group;
-    const int blk_kv_end = min(a.kv_len, a.query_start + pt_max * kRows + kRows);
+    const int pt_max = a.n_pos_tiles - 1 - (rblk * kPfWaves) / a.group;
+    const int blk_kv_end = min(a.kv_len, a.query_start + pt_max * kPfRows + kPfRows);
     const int ntiles = (blk_kv_end + kPfBN - 1) / kPfBN;
-    const int wave_kv_end = task_ok ? min(a.kv_len, pos0 + kRows) : 0;
+    const int wave_kv_end = task_ok ? min(a.kv_len, pos0 + kPfRows) : 0;
     const int wave_tiles = (wave_kv_end + kPfBN - 1) / kPfBN;
 
     const uint16_t* kh = a.k_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
@@ -159,38 +185,51 @@ __global__ __launch_bounds__(WAVES * kWave, 1) void attn_prefill_kernel(PrefillA
         }
     };
 
+    // Tiles 0 and 1 are copied ahead; tile t+2 is issued in the phase that
+    // first reads tile t, into the stage of tile t-2, whose last reader (group
+    // B's PV of tile t-2) ended with the phase before.
     if (ntiles > 0) issue_tile(0, 0);
     if (ntiles > 1) issue_tile(1, 1);
 
-    // Q^T (B operand): qop[nb][kk] = Q[row0 + 32nb + l32][16kk + 8hl + 0..7].
-    half8_t qop[NBK][8];
-#pragma unroll
-    for (int nbk = 0; nbk < NBK; ++nbk) {
-        const int row = row0 + 32 * nbk + l32;
+    // Q^T (B operand): qop[kk] = Q[row0 + l32][16kk + 8hl + 0..7].
+    half8_t qop[8];
+    {
+        const int row = row0 + l32;
         const bool ok = task_ok && row < a.q_len;
         const uint16_t* qr = a.q + (static_cast<int64_t>(ok ? row : 0) * a.num_q_heads + qh) * kHeadDim;
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) qop[nbk][kk] = load_half8(qr + 16 * kk + 8 * hl);
+        for (int kk = 0; kk < 8; ++kk) qop[kk] = load_half8(qr + 16 * kk + 8 * hl);
         if (!ok) {
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) qop[nbk][kk] = half8_t{};
+            for (int kk = 0; kk < 8; ++kk) qop[kk] = half8_t{};
         }
     }
+    // Settle the Q loads here.  The compiler's wait insertion does not see the
+    // asm DMAs, so a Q load still pending at the loop would make it wait
+    // for Q inside the loop with a vmcnt that, counted by the hardware, also
+    // covers the next tile's copies: one stall per tile.  The asm "use" makes
+    // it wait once, before the loop.
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) asm volatile("" : "+v"(qop[kk]));
 
-    float16_t o[4][NBK];
+    float16_t o[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int nbk = 0; nbk < NBK; ++nbk)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[db][nbk][r] = 0.0f;
-    float m_run[NBK], l_run[NBK];
-#pragma unroll
-    for (int nbk = 0; nbk < NBK; ++nbk) {
-        m_run[nbk] = kPfNegBig;
-        l_run[nbk] = 0.0f;
-    }
+        for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+    float m_run = kPfNegBig, l_run = 0.0f;
     const float c = a.scale_log2;
+    float16_t s[2];  // S^T of the tile in flight
+    half8_t pop[4];  // P^T of the last softmaxed tile
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pop[k] = half8_t{};
+    // The V half of the last stage is what GEMM(0) multiplies with P = 0:
+    // zero it (finite), before the first barrier.  Tile 3 refills it only
+    // after both groups are past GEMM(0).
+    {
+        uint4_t* vz = reinterpret_cast<uint4_t*>(pf_lds + (kPfStages - 1) * kPfStageBytes + kPfKBytes);
+        for (int i = tid; i < kPfVBytes / 16; i += kPfWaves * kWave) vz[i] = uint4_t{0u, 0u, 0u, 0u};
+    }
 
     // Per-lane LDS read offsets.  K (A operand of S^T = K Q^T): key 32mb + l32,
     // dims 16kk + 8hl.  V^T (A operand of O^T += V^T P^T) via the transposing
@@ -200,133 +239,168 @@ __global__ __launch_bounds__(WAVES * kWave, 1) void attn_prefill_kernel(PrefillA
     const uint32_t k_lane = (l32 & 15) * kPfKBlock + (l32 >> 4) * 256 + 16 * hl;
     const uint32_t v_lane = (4 * (gi >> 1) + (ii >> 2)) * kPfVBlock + 32 * (gi & 1) + 8 * (ii & 3);
 
-    for (int j = 0; j < ntiles; ++j) {
-        const int st = j % kPfStages;
-        // Tile j is in LDS for this wavefront once at most the copies of tile
-        // j+1 (issued last iteration; vector-memory loads retire in order) are
-        // outstanding.
-        if (j + 1 < ntiles) {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kDmaPerWave));
-        } else {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    // GEMM phase of tile j: O^T += V^T P^T of tile j-1 (MFMA slots 0-15:
+    // key step i/4, dim block i%4), then S^T = K Q^T of tile j (slots 16-31:
+    // dim step (i-16)/2, key block i%2).  One software pipeline over the 32
+    // slots: each slot's LDS operand is read kPfAhead slots before its MFMA
+    // into a ring of registers, so LDS latency hides behind ~kPfAhead MFMAs;
+    // a scheduling fence per slot keeps that order.
+    //
+    // Every GEMM phase runs all 32 slots (one code path keeps register
+    // allocation tight): at j = 0 the PV half multiplies P = 0 with the V
+    // stage zeroed below (adds exactly +0 to O); at j = wave_tiles the S half
+    // reads a stage inside LDS and its result is never used.
+    auto gemm_phase = [&](int j) {
+        if (j > wave_tiles) return;
+        constexpr int kRing = kPfAhead + 1;
+        const unsigned char* vb = pf_lds + ((j + kPfStages - 1) % kPfStages) * kPfStageBytes + kPfKBytes + v_lane;
+        const unsigned char* kb = pf_lds + (j % kPfStages) * kPfStageBytes + k_lane;
+        auto read_op = [&](int i) {
+            if (i < 16) {
+                // V^T[32 dims of block i%4, 16 keys of step i/4].
+                const unsigned char* p0 = vb + 256 * (i >> 2) + 64 * (i & 3);
+                return cat(lds_read_tr16(reinterpret_cast<const half_t*>(p0)),
+                           lds_read_tr16(reinterpret_cast<const half_t*>(p0 + 8 * kPfVBlock)));
+            }
+            // K[32 keys of block i%2, 16 dims of step (i-16)/2].
+            return *reinterpret_cast<const half8_t*>(kb + 512 * (i & 1) + 32 * ((i - 16) >> 1));
+        };
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[mb][r] = 0.0f;
+        half8_t ring[kRing];
+#pragma unroll
+        for (int i = 0; i < kPfAhead; ++i) ring[i % kRing] = read_op(i);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            if (i + kPfAhead < 32) ring[(i + kPfAhead) % kRing] = read_op(i + kPfAhead);
+            if (i < 16) {
+                o[i & 3] = mfma32x32x16(ring[i % kRing], pop[i >> 2], o[i & 3]);
+            } else {
+                s[i & 1] = mfma32x32x16(ring[i % kRing], qop[(i - 16) >> 1], s[i & 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        // Every wavefront is past tile j-1, so its stage can be refilled.
-        if (j + 2 < ntiles) issue_tile(j + 2, (j + 2) % kPfStages);
+    };
 
-        if (j < wave_tiles) {
-            const unsigned char* kb = pf_lds + st * kPfStageBytes;
-            const unsigned char* vb = kb + kPfKBytes;
-            const int n0 = j * kPfBN;
-
-            // S^T[mb][nb]: rows = keys n0 + 32mb + 8(r/4) + 4hl + r%4, col = query row.
-            float16_t s[2][NBK];
+    // Softmax phase of tile j: mask, running max (lazy), P = 2^(c*s - m), row sum.
+    auto softmax_phase = [&](int j) {
+        if (j < 0 || j >= wave_tiles) return;
+        const int n0 = j * kPfBN;
+        const bool need_mask = (n0 + kPfBN - 1 > pos0) || (n0 + kPfBN > a.kv_len);
+        if (need_mask) {
+            const int qpos = pos0 + l32;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int nbk = 0; nbk < NBK; ++nbk)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) s[mb][nbk][r] = 0.0f;
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    const half8_t ka = *reinterpret_cast<const half8_t*>(kb + k_lane + 512 * mb + 32 * kk);
-#pragma unroll
-                    for (int nbk = 0; nbk < NBK; ++nbk) s[mb][nbk] = mfma32x32x16(ka, qop[nbk][kk], s[mb][nbk]);
+                for (int r = 0; r < 16; ++r) {
+                    const int n = n0 + 32 * mb + 8 * (r >> 2) + 4 * hl + (r & 3);
+                    if (n > qpos || n >= a.kv_len) s[mb][r] = kPfNegBig;
                 }
-            }
+        }
+        // P = 2^(c*s - m) with the running max m as it stands; the row sum
+        // runs in four independent f32 chains.
+        auto exp_tile = [&](float m_use) {
+            float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[mb][r], c, -m_use));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 1], c, -m_use));
+                    ps[(r >> 1) & 3] += p0 + p1;
+                    pop[2 * mb + (r >> 3)][r & 7] = static_cast<half_t>(p0);
+                    pop[2 * mb + (r >> 3)][(r & 7) + 1] = static_cast<half_t>(p1);
+                }
+            return (ps[0] + ps[1]) + (ps[2] + ps[3]);
+        };
+        float psum = exp_tile(m_run);
+        // The max is only raised when P would leave f16 range: a lane's partial
+        // row sum below 2^15 bounds each of its p below 2^15 (the test also
+        // catches inf).  Then the tile's row max becomes the running max, O and
+        // l are rescaled and P is recomputed.  Until then p <= 2^15 keeps full
+        // f16 relative precision, so the normalised result is the same function.
+        if (__any(!(psum < kPfPsumLimit))) {
+            float mx = kPfNegBig;
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
+            mx = fmaxf(mx, swap_halves(mx));
+            const float m_new = fmaxf(m_run, mx * c);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+            m_run = m_new;
+            psum = exp_tile(m_run);
+        }
+        l_run += psum;
+    };
 
-            const bool need_mask = (n0 + kPfBN - 1 > pos0) || (n0 + kPfBN > a.kv_len);
-            half8_t pop[4][NBK];
-#pragma unroll
-            for (int nbk = 0; nbk < NBK; ++nbk) {
-                if (need_mask) {
-                    const int qpos = pos0 + 32 * nbk + l32;
-#pragma unroll
-                    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int n = n0 + 32 * mb + 8 * (r >> 2) + 4 * hl + (r & 3);
-                            if (n > qpos || n >= a.kv_len) s[mb][nbk][r] = kPfNegBig;
-                        }
-                }
-                float mx = kPfNegBig;
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mb][nbk][r]);
-                mx = fmaxf(mx, swap_halves(mx));
-                const float m_cand = mx * c;
-                if (__any(m_cand > m_run[nbk] + kPfRescaleSlack)) {
-                    const float m_new = fmaxf(m_run[nbk], m_cand);
-                    const float alpha = __builtin_amdgcn_exp2f(m_run[nbk] - m_new);
-                    l_run[nbk] *= alpha;
-#pragma unroll
-                    for (int db = 0; db < 4; ++db) o[db][nbk] *= alpha;
-                    m_run[nbk] = m_new;
-                }
-                const float m_use = m_run[nbk];
-                float psum = 0.0f;
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float p = __builtin_amdgcn_exp2f(fmaf(s[mb][nbk][r], c, -m_use));
-                        psum += p;
-                        pop[2 * mb + (r >> 3)][nbk][r & 7] = static_cast<half_t>(p);
-                    }
-                l_run[nbk] += psum;
+    // Global phase 2t: group A runs GEMM(t), group B softmax(t-1); phase
+    // 2t+1: A softmax(t), B GEMM(t).  GEMM(ntiles) is the last PV; softmax of
+    // a tile outside the wavefront's range is a no-op.  Each group has its own
+    // straight-line loop (B's is A's rotated by one phase); both pass the
+    // same 2*(ntiles+1) barriers.
+    static_assert(kPfStages == 4, "the wait below assumes one tile in flight behind tile t");
+    auto open_even_phase = [&](int t) {
+        if (t < ntiles) {
+            // Tile t is in LDS once at most the copies of tile t+1 are
+            // outstanding (vector-memory loads retire in order).
+            if (t + 1 < ntiles) {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kDmaPerWave));
+            } else {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
             }
-
-            // O^T[db][nb] += V^T[32 dims, 16 keys] P^T[16 keys, 32 rows], 4 key steps.
-#pragma unroll
-            for (int ks2 = 0; ks2 < 4; ++ks2) {
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const unsigned char* p0 = vb + v_lane + 256 * ks2 + 64 * db;
-                    const half8_t va = cat(lds_read_tr16(reinterpret_cast<const half_t*>(p0)),
-                                           lds_read_tr16(reinterpret_cast<const half_t*>(p0 + 8 * kPfVBlock)));
-#pragma unroll
-                    for (int nbk = 0; nbk < NBK; ++nbk) o[db][nbk] = mfma32x32x16(va, pop[ks2][nbk], o[db][nbk]);
-                }
-            }
+        }
+        pf_barrier();
+        if (t + 2 < ntiles) issue_tile(t + 2, (t + 2) % kPfStages);
+    };
+    if (grp == 0) {
+        for (int t = 0; t <= ntiles; ++t) {
+            open_even_phase(t);
+            gemm_phase(t);
+            pf_barrier();
+            softmax_phase(t);
+        }
+    } else {
+        for (int t = 0; t <= ntiles; ++t) {
+            open_even_phase(t);
+            softmax_phase(t - 1);
+            pf_barrier();
+            gemm_phase(t);
         }
     }
 
     if (!task_ok) return;
     // out[row][d] with d = 32db + 8(r/4) + 4hl + r%4.
+    const int row = row0 + l32;
+    const float lt = l_run + swap_halves(l_run);
+    const float l_safe = fmaxf(lt, 1.0e-8f);
+    if (row < a.q_len) {
+        uint16_t* orow = a.out + (static_cast<int64_t>(row) * a.num_q_heads + qh) * kHeadDim;
 #pragma unroll
-    for (int nbk = 0; nbk < NBK; ++nbk) {
-        const int row = row0 + 32 * nbk + l32;
-        const float lt = l_run[nbk] + swap_halves(l_run[nbk]);
-        const float l_safe = fmaxf(lt, 1.0e-8f);
-        if (row < a.q_len) {
-            uint16_t* orow = a.out + (static_cast<int64_t>(row) * a.num_q_heads + qh) * kHeadDim;
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+            for (int i = 0; i < 4; ++i) {
+                half4_t h;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    half4_t h;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) h[e] = static_cast<half_t>(o[db][nbk][4 * i + e] / l_safe);
-                    *reinterpret_cast<half4_t*>(orow + 32 * db + 8 * i + 4 * hl) = h;
-                }
-        }
+                for (int e = 0; e < 4; ++e) h[e] = static_cast<half_t>(o[db][4 * i + e] / l_safe);
+                *reinterpret_cast<half4_t*>(orow + 32 * db + 8 * i + 4 * hl) = h;
+            }
     }
 }
 
-template <int NBK, int WAVES>
 static int32_t launch_prefill(PrefillArgs a, int num_kv_heads, hipStream_t stream) {
-    constexpr int kRows = 32 * NBK;
-    a.n_pos_tiles = (a.q_len + kRows - 1) / kRows;
+    a.n_pos_tiles = (a.q_len + kPfRows - 1) / kPfRows;
     a.tasks_per_head = a.n_pos_tiles * a.group;
-    a.blocks_per_head = (a.tasks_per_head + WAVES - 1) / WAVES;
+    a.blocks_per_head = (a.tasks_per_head + kPfWaves - 1) / kPfWaves;
     const int64_t blocks = static_cast<int64_t>(a.blocks_per_head) * num_kv_heads;
     if (blocks > 0x7fffffff) return GROUT_ERR_KV_LEN;
-    hipLaunchKernelGGL((attn_prefill_kernel<NBK, WAVES>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(WAVES * kWave), 0, stream, a);
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kPfWaves * kWave), 0, stream, a);
     return launch_status();
 }
 
@@ -367,8 +441,5 @@ extern "C" int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache
     a.kv_len = kv_len;
     a.query_start = query_start;
     a.max_seq_len = max_seq_len;
-    // 8 wavefronts x 32 query rows: two wavefronts per SIMD, so one's softmax
-    // (VALU, v_exp_f32) overlaps the other's MFMAs; LDS reads stay below the
-    // measured ~125-160 B/clk/CU.
-    return launch_prefill<1, 8>(a, num_kv_heads, to_hip(stream));
+    return launch_prefill(a, num_kv_heads, to_hip(stream));
 }
