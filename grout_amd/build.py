@@ -30,6 +30,10 @@ HIP_FLAGS = [
     "-Wall",
     "-Wno-unused-result",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Single-lane counter RMWs stay plain atomics: the wave-aggregating rewrite
+    # consumes the returned value right after issue, i.e. waits a memory round
+    # trip where the kernel only needs the value at its end.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-I", os.path.join(ROOT, "include"),
     "-I", CSRC,
 ]

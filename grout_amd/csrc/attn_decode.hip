@@ -34,8 +34,9 @@
 //    position also writes its K/V row to the cache before streaming.  The
 //    last workgroup of a KV head merges the splits, found with a counter;
 //    the partials travel through agent-coherent (sc1) stores and loads so no
-//    L2-wide writeback/invalidate is needed; the last head advances the
-//    device position when asked to.
+//    L2-wide writeback/invalidate is needed.  When asked to, the workgroup
+//    holding the last position ticket (taken right after the position read)
+//    advances the device position.
 #include <math.h>
 
 #include "abi_util.h"
@@ -120,6 +121,18 @@ __device__ __forceinline__ void dec_lds_dma16_ptr(const void* gptr, uint32_t lds
         : "memory");
 }
 
+// Same copy, device-coherent (sc1): reads data that workgroups on other
+// XCDs wrote with sc1 stores, past any stale line in this XCD's L2.
+__device__ __forceinline__ void dec_lds_dma16_ptr_sc1(const void* gptr, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, off sc1"
+        :
+        : "v"(gptr), "s"(lds_base)
+        : "memory");
+}
+
 constexpr int dec_waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
 // Per-workgroup inputs staged into LDS ahead of the K/V stream, 256 B rows:
@@ -185,13 +198,6 @@ __device__ __forceinline__ void store16_agent(uint16_t* p, half8_t v) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) __hip_atomic_store(q + i, u[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ half8_t load16_agent(const uint16_t* p) {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    uint4_t u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) u[i] = __hip_atomic_load(q + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return __builtin_bit_cast(half8_t, u);
-}
 
 __device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
@@ -219,6 +225,19 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     const uint32_t pos = pos_raw < static_cast<uint32_t>(a.max_seq_len) ? pos_raw
                                                                          : a.max_seq_len - 1;
     const int s_kv = static_cast<int>(pos) + 1;
+    // Position advance: each workgroup takes a ticket once its position read
+    // has completed (the asm consumes the loaded value; its memory clobber
+    // keeps the RMW behind it).  The holder of the last ticket knows every
+    // workgroup has read the position and stores position+1 when it ends;
+    // the RMW's latency overlaps the K/V stream instead of the merge.
+    uint32_t ticket = 0xffffffffu;
+    if constexpr (kFused) {
+        if (a.advance_position && tid == 0) {
+            asm volatile("" ::"s"(pos_raw) : "memory");
+            ticket = __hip_atomic_fetch_add(&a.counters[a.num_kv_heads * kDecCounterStride], 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     const int tiles = (s_kv + a.block_n - 1) / a.block_n;
     const int per = (tiles + a.num_splits - 1) / a.num_splits;
     const int tb = split * per;
@@ -519,6 +538,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     }
 
     if constexpr (kFused) {
+        const uint32_t last_ticket = static_cast<uint32_t>(a.num_splits) * static_cast<uint32_t>(a.num_kv_heads) - 1u;
+        if (a.advance_position && tid == 0 && ticket == last_ticket) {
+            __hip_atomic_store(&a.counters[a.num_kv_heads * kDecCounterStride], 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.position_w, pos_raw + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         // Last workgroup of this KV head merges its splits.  Every partial is
         // complete at the coherence point (sc1 stores, vmcnt(0)) before this
         // workgroup's counter increment; the merging workgroup reads them with
@@ -531,104 +556,116 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             uint32_t flag = 0;
             if (prev + 1 == static_cast<uint32_t>(a.num_splits)) {
                 flag = 1;
-                // This head is complete: reset its counter for the next launch
-                // and count it towards the position advance (the RMW's latency
-                // overlaps the merge below).
+                // This head is complete: reset its counter for the next launch.
                 __hip_atomic_store(&a.counters[kvh * kDecCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint32_t heads = __hip_atomic_fetch_add(&a.counters[a.num_kv_heads * kDecCounterStride], 1u,
-                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (heads + 1 == static_cast<uint32_t>(a.num_kv_heads)) {
-                    __hip_atomic_store(&a.counters[a.num_kv_heads * kDecCounterStride], 0u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                    // Every workgroup has read the position by now.
-                    if (a.advance_position)
-                        __hip_atomic_store(a.position_w, pos_raw + 1u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
             }
             s_flag = flag;
         }
         lds_barrier();
         if (s_flag == 0) return;
 
-        // Merge of this KV head: O[g] = sum_s w_s O_s[g], w_s = 2^(lse_s - M)/sum.
-        // Thread t owns head g = (t/16) % G, 16-byte dim chunk j = t % 16 and the
-        // splits s = sg, sg+SG, ... (sg = (t/16)/G, SG = 16/G); all of its LSE
-        // and partial loads go out together (one memory round trip per batch of
-        // kMergeBatch splits), and max, sum and the split groups are reduced
-        // through LDS.
-        constexpr int kMergeBatch = 16;
+        // Merge of this KV head: O[g] = sum_s w_s O_s[g] / sum_s w_s with
+        // w_s = 2^(lse_s - M), the combination of attn_decode_merge_kernel.
+        // The head's partial rows are contiguous (row s*G + g); batches of up
+        // to kMergeRows rows go straight into the free stage buffers with
+        // device-coherent (sc1) copies, and their LSEs arrive with sc1 dword
+        // loads into a transposed [g][split] table (padded with -1e30), one
+        // memory round trip per batch.  Thread t owns row g = it/32 and dims
+        // 4(it%32)..+3 for it = t, t+256 (G <= 16); per 32 splits it reads
+        // its LSEs as 16-byte vectors, then accumulates with independent
+        // LDS reads, keeping an online (max, sum, acc) across chunks.
+        constexpr int kMergeRows = 448;
+        static_assert(kMergeRows * 256 + (kMergeRows + 31 * GROUT_MAX_DECODE_GROUP) * 4 <= kDecStages * kDecStageBytes,
+                      "merge batch must fit the stages");
+        static_assert(GROUT_MAX_DECODE_GROUP * 32 <= 2 * kDecThreads, "two merge items per thread");
         const int NS = a.num_splits;
-        const int SG = 16 / G;
-        const int g = (tid >> 4) % G, j = tid & 15, sg = (tid >> 4) / G;
-        const bool active = sg < SG;
-        const float* lse = a.lse_partial + static_cast<int64_t>(kvh) * NS * G;
-        const uint16_t* src = a.att_partial + (static_cast<int64_t>(kvh) * NS * G + g) * kHeadDim + 8 * j;
-        float* red_m = reinterpret_cast<float*>(lds);  // [16][16] per (sg, g) max
-        float* red_s = red_m + 256;                    // [16][16] per (sg, g) sum
-        float* part = red_s + 256;                     // [16][16][128] per (sg, g) partial O
-        // Each thread keeps an online (max, sum, acc) over its splits; the
-        // split groups are rescaled to the head's max when combined.
-        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        float m_loc = -INFINITY, s_loc = 0.0f;
-        for (int s0 = sg; active && s0 < NS; s0 += kMergeBatch * SG) {
-            half8_t x[kMergeBatch];
-            float lv[kMergeBatch];
+        const int SB = kMergeRows / G;        // splits per batch
+        const int SBp = (SB + 31) & ~31;      // row length of the LSE table
+        const uint16_t* part_h = a.att_partial + static_cast<int64_t>(kvh) * NS * G * kHeadDim;
+        const float* lse_h = a.lse_partial + static_cast<int64_t>(kvh) * NS * G;
+        const unsigned char* rows_l = lds;
+        float* lse_t = reinterpret_cast<float*>(lds + kMergeRows * 256);
+        float m_i[2] = {-INFINITY, -INFINITY}, s_i[2] = {0.0f, 0.0f};
+        float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        for (int s0 = 0; s0 < NS; s0 += SB) {
+            const int ns_b = min(SB, NS - s0);
+            const int rows = ns_b * G;
+            const uint16_t* src = part_h + static_cast<int64_t>(s0) * G * kHeadDim;
+            // Copy i moves rows 4i..4i+3 (lane l: row 4i + l/16, 16-byte chunk
+            // l%16) to LDS byte 1024i + 16l; pad lanes re-read the last row.
+            const int ncopies = (rows + 3) / 4;
+            for (int i = wave; i < ncopies; i += kDecWaves) {
+                const int r = min(4 * i + (lane >> 4), rows - 1);
+                dec_lds_dma16_ptr_sc1(src + static_cast<int64_t>(r) * kHeadDim + 8 * (lane & 15), lds0 + 1024u * i);
+            }
+            for (int i = tid; i < G * SBp; i += kDecThreads) {
+                const int g = i / SBp, sp = i - g * SBp;
+                float v = kNegBig;
+                if (sp < ns_b)
+                    v = __hip_atomic_load(lse_h + static_cast<int64_t>(s0 + sp) * G + g, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+                lse_t[i] = v;
+            }
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
+            lds_barrier();
 #pragma unroll
-            for (int u = 0; u < kMergeBatch; ++u) {
-                const int s2 = s0 + u * SG;
-                lv[u] = -INFINITY;
-                if (s2 < NS) {
-                    x[u] = load16_agent(src + static_cast<int64_t>(s2) * G * kHeadDim);
-                    lv[u] = __hip_atomic_load(lse + s2 * G + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int k = 0; k < 2; ++k) {
+                const int it = tid + kDecThreads * k;
+                if (it < G * 32) {
+                    const int g = it >> 5, c = it & 31;
+                    const float* lrow = lse_t + g * SBp;
+                    const unsigned char* rbase = rows_l + g * 256 + 8 * c;
+                    for (int sc = 0; sc < ns_b; sc += 32) {
+                        float lv[32];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            const float4_t v4 = *reinterpret_cast<const float4_t*>(lrow + sc + 4 * u);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) lv[4 * u + e] = v4[e];
+                        }
+                        float mb = m_i[k];
+#pragma unroll
+                        for (int u = 0; u < 32; ++u) mb = fmaxf(mb, lv[u]);
+                        const float r = (m_i[k] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_i[k] - mb);
+                        s_i[k] *= r;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[k][e] *= r;
+                        m_i[k] = mb;
+                        const int nu = min(32, ns_b - sc);
+                        if (nu == 32) {
+#pragma unroll
+                            for (int u = 0; u < 32; ++u) {
+                                const float w = __builtin_amdgcn_exp2f(lv[u] - mb);
+                                s_i[k] += w;
+                                const half4_t x = *reinterpret_cast<const half4_t*>(rbase + (sc + u) * G * 256);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[k][e] += w * static_cast<float>(x[e]);
+                            }
+                        } else {
+                            for (int u = 0; u < nu; ++u) {
+                                const float w = __builtin_amdgcn_exp2f(lv[u] - mb);
+                                s_i[k] += w;
+                                const half4_t x = *reinterpret_cast<const half4_t*>(rbase + (sc + u) * G * 256);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[k][e] += w * static_cast<float>(x[e]);
+                            }
+                        }
+                    }
                 }
             }
-            float mb = m_loc;
-#pragma unroll
-            for (int u = 0; u < kMergeBatch; ++u) mb = fmaxf(mb, lv[u]);
-            const float r = (m_loc == -INFINITY) ? 0.0f : exp2f(m_loc - mb);
-            s_loc *= r;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] *= r;
-            m_loc = mb;
-#pragma unroll
-            for (int u = 0; u < kMergeBatch; ++u) {
-                if (s0 + u * SG < NS) {
-                    const float w = exp2f(lv[u] - m_loc);
-                    s_loc += w;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) o[e] += static_cast<float>(x[u][e]) * w;
-                }
-            }
+            lds_barrier();  // the next batch overwrites the rows
         }
-        if (active) {
-            if (j == 0) {
-                red_m[sg * 16 + g] = m_loc;
-                red_s[sg * 16 + g] = s_loc;
-            }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) part[(sg * 16 + g) * kHeadDim + 8 * j + e] = o[e];
-        }
-        lds_barrier();
-        if (tid < G * 16) {
-            const int gg = tid >> 4, jj = tid & 15;
-            float M = -INFINITY;
-            for (int q2 = 0; q2 < SG; ++q2) M = fmaxf(M, red_m[q2 * 16 + gg]);
-            float sum = 0.0f, f[16];
-            for (int q2 = 0; q2 < SG; ++q2) {
-                const float mq = red_m[q2 * 16 + gg];
-                f[q2] = (mq == -INFINITY) ? 0.0f : exp2f(mq - M);
-                sum += red_s[q2 * 16 + gg] * f[q2];
-            }
-            const float inv = 1.0f / fmaxf(sum, 1.0e-8f);
-            half8_t ho;
+        for (int k = 0; k < 2; ++k) {
+            const int it = tid + kDecThreads * k;
+            if (it < G * 32) {
+                const int g = it >> 5, c = it & 31;
+                const float inv = 1.0f / fmaxf(s_i[k], 1.0e-8f);
+                half4_t h;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float x = 0.0f;
-                for (int q2 = 0; q2 < SG; ++q2) x += part[(q2 * 16 + gg) * kHeadDim + 8 * jj + e] * f[q2];
-                ho[e] = static_cast<half_t>(x * inv);
+                for (int e = 0; e < 4; ++e) h[e] = static_cast<half_t>(acc[k][e] * inv);
+                *reinterpret_cast<half4_t*>(a.out + (static_cast<int64_t>(kvh) * G + g) * kHeadDim + 4 * c) = h;
             }
-            store_half8(a.out + (static_cast<int64_t>(kvh) * G + gg) * kHeadDim + 8 * jj, ho);
         }
     }
 }
