@@ -412,8 +412,16 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     const uint32_t v_lane = (4 * qgrp + (n >> 2)) * kDecVBlock + wave * 256 + 8 * (n & 3);
 
     for (int c = 0; c < nchunks; ++c) {
+        if (c >= 1) {
+            // Every wavefront is past chunk c-1, whose stage now takes chunk
+            // c+3 (chunks 0..3 were issued before the loop); the copy goes
+            // out before this wavefront waits for chunk c.
+            lds_barrier();
+            if (c + kDecStages - 1 < nchunks) issue_chunk(c + kDecStages - 1);
+        }
         // Chunk c has landed once only the copies of the chunks issued after
-        // it (8 per wave each; up to three) are outstanding.
+        // it (8 per wave each: chunks c+1..c+3 where they exist) are
+        // outstanding.
         const int younger = min(kDecStages - 1, nchunks - 1 - c);
         if (younger >= 3) {
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(6 * kDecDmaPerWave));
@@ -425,9 +433,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
         }
         lds_barrier();
-        // Every wavefront is past chunk c-1, whose stage now takes chunk c+3
-        // (chunks 0..3 were issued before the loop).
-        if (c >= 1 && c + kDecStages - 1 < nchunks) issue_chunk(c + kDecStages - 1);
         if (c == c_pos) {
             // The copy of this chunk read the cache before the new row was
             // stored; put the new K/V row into its LDS slot.
