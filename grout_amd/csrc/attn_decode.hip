@@ -57,6 +57,8 @@ constexpr int kDecStages = 4;
 constexpr int kDecDmaPerWave = 16 / kDecWaves;  // 1 KB copies of K (and of V) per wave
 constexpr int kDecRedStride = 16 * kHeadDim + 32;   // floats per wave in the final combine
 constexpr float kNegBig = -1.0e30f;
+// Lazy rescale slack of the decode softmax (log2 units): p <= 2^8.
+constexpr float kDecRescaleSlack = 8.0f;
 // Merge counters sit in separate 256-byte lines so the heads' atomics do not
 // serialise on one line.
 constexpr int kDecCounterStride = 64;  // u32 elements
@@ -99,12 +101,13 @@ struct DecodeArgs {
 // lds_base + 16*l.  Inline asm keeps the compiler from serialising the copies
 // behind vmcnt(0) waits; the kernel waits for them with s_waitcnt vmcnt before
 // its workgroup barrier.  M0 carries the LDS base; one wait state separates
-// the M0 write from the copy.
+// the M0 write from the copy.  The K/V stream is read once per step, so the
+// copies carry the non-temporal hint.
 __device__ __forceinline__ void dec_lds_dma16(const void* gbase, uint32_t voff, uint32_t lds_base) {
     asm volatile(
         "s_mov_b32 m0, %2\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %0, %1"
+        "global_load_lds_dwordx4 %0, %1 nt"
         :
         : "v"(voff), "s"(gbase), "s"(lds_base)
         : "memory");
@@ -470,22 +473,31 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, swap_halves(mx));
-            const float m_new = fmaxf(m, mx);
-            const float alpha = exp2f(m - m_new);
+            // Lazy rescale: the running max m moves only when a score exceeds
+            // it by more than kDecRescaleSlack, so p = 2^(s - m) <= 2^8 stays
+            // well inside f16 and the (rare) rescale of acc and l is the only
+            // place they leave the matrix-core registers.
+            if (__any(mx > m + kDecRescaleSlack)) {
+                const float m_new = fmaxf(m, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+                l *= alpha;
+#pragma unroll
+                for (int db = 0; db < 8; ++db) acc[db] *= alpha;
+                m = m_new;
+            }
             float psum = 0.0f;
             half4_t pop;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = exp2f(s[r] - m_new);
+                const float p = __builtin_amdgcn_exp2f(s[r] - m);
                 psum += p;
                 pop[r] = static_cast<half_t>(p);
             }
-            l = l * alpha + psum;
-            m = m_new;
+            l += psum;
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
                 const half4_t vop = lds_read_tr16(reinterpret_cast<const half_t*>(vb + v_lane + 32 * db));
-                acc[db] = mfma16x16x16(vop, pop, acc[db] * alpha);
+                acc[db] = mfma16x16x16(vop, pop, acc[db]);
             }
         }
     }
