@@ -34,6 +34,10 @@ HIP_FLAGS = [
     # consumes the returned value right after issue, i.e. waits a memory round
     # trip where the kernel only needs the value at its end.
     "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
+    # MFMAs accumulate in ordinary VGPRs: the decode accumulators are also
+    # touched by VALU (rare rescale), and the AGPR form would copy them into
+    # and out of the accumulation registers around every MFMA.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"),
     "-I", CSRC,
 ]

@@ -46,15 +46,21 @@ namespace grout {
 
 constexpr int kDecWaves = 4;
 constexpr int kDecThreads = kDecWaves * kWave;
-constexpr int kDecSub = 16;                     // tokens per wavefront per chunk
-constexpr int kDecChunk = kDecWaves * kDecSub;  // 64 tokens per chunk
-constexpr int kDecKBlock = 4 * 256 + 16;        // 4 rows of 256 B + pad (K)
-constexpr int kDecVBlock = 4 * 256 + 32;        // 4 rows of 256 B + pad (V)
-constexpr int kDecKBytes = 16 * kDecKBlock;
-constexpr int kDecVBytes = 16 * kDecVBlock;
-constexpr int kDecStageBytes = kDecKBytes + kDecVBytes;
-constexpr int kDecStages = 4;
-constexpr int kDecDmaPerWave = 16 / kDecWaves;  // 1 KB copies of K (and of V) per wave
+// Each wavefront streams its own 16-token sub-chunks (sub-chunks w, w+4, ...
+// of the split) through a private ring of kDecWaveStages stages; a stage is
+// the sub-chunk's K rows (4 KB) then its V rows (4 KB).  No workgroup barrier
+// is needed inside the stream.
+constexpr int kDecSubTok = 16;
+constexpr int kDecSubBytes = kDecSubTok * 256;
+constexpr int kDecWaveStages = 4;
+constexpr int kDecWaveBytes = kDecWaveStages * 2 * kDecSubBytes;
+constexpr int kDecLdsBytes = kDecWaves * kDecWaveBytes;
+constexpr int kDecMinSplitTokens = 64;
+// Chunk swizzle of a 256-byte token row in a stage: LDS chunk c of row tr
+// holds global chunk c ^ dec_swz(tr).  Distinct over the 16 rows (K reads:
+// one row per lane) and, for the transposing V reads, spreading each 32-lane
+// half over all 64 banks.
+__device__ __forceinline__ int dec_swz(int tr) { return 2 * (tr & 7) + (tr >> 3); }
 constexpr int kDecRedStride = 16 * kHeadDim + 32;   // floats per wave in the final combine
 constexpr float kNegBig = -1.0e30f;
 // Lazy rescale slack of the decode softmax (log2 units): p <= 2^8.
@@ -63,7 +69,7 @@ constexpr float kDecRescaleSlack = 8.0f;
 // serialise on one line.
 constexpr int kDecCounterStride = 64;  // u32 elements
 
-static_assert(kDecWaves * kDecRedStride * 4 <= kDecStages * kDecStageBytes,
+static_assert(kDecWaves * kDecRedStride * 4 <= kDecLdsBytes,
               "wave combine reuses the stage buffers");
 
 struct DecodeArgs {
@@ -208,7 +214,7 @@ __device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t 
 
 template <bool kFused>
 __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs a) {
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[kDecStages * kDecStageBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kDecLdsBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char pro[kDecProDmas * 1024];
     __shared__ __attribute__((aligned(16))) half_t q_lds[GROUT_MAX_DECODE_GROUP * kHeadDim];
     __shared__ float s_cos[64], s_sin[64];
@@ -247,35 +253,35 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     const int te = min(tb + per, tiles);
     const int tok_begin = tb * a.block_n;
     const int tok_end = (tb < te) ? min(te * a.block_n, s_kv) : tok_begin;
-    const int nchunks = (tok_end - tok_begin + kDecChunk - 1) / kDecChunk;
+    const int nsub = (tok_end - tok_begin + kDecSubTok - 1) / kDecSubTok;
+    const int nk = nsub > wave ? (nsub - wave + kDecWaves - 1) / kDecWaves : 0;  // this wave's sub-chunks
 
     const uint16_t* kh = a.k_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
     const uint16_t* vh = a.v_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
 
-    // Chunk copy: K/V block b (tokens b + 16*row, rows 0..3) of a chunk is one
-    // 1 KB copy; this wavefront moves blocks 4*wave..4*wave+3.  Lane l covers
-    // row l/16, 16-byte column l%16.  Rows at or past tok_end are clamped to
-    // tok_end-1 (their scores are masked).
+    // Sub-chunk copy: this wavefront's k-th sub-chunk (tokens t0 + [0,16),
+    // t0 = tok_begin + 16*(wave + 4k)) lands in its stage k%4.  Copy i moves
+    // token rows 4i..4i+3: 1 KB contiguous in the cache, 1 KB contiguous in
+    // LDS.  Lane l takes row tr = 4i + l/16 and source chunk (l%16) ^ swz(tr),
+    // so LDS chunk c of row tr holds global chunk c ^ swz(tr): the MFMA operand
+    // reads below are bank-conflict free without padding.  Rows at or past
+    // tok_end repeat row tok_end-1 (their scores are masked).
     const uint32_t lds0 = static_cast<uint32_t>(
         (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(lds)));
-    const uint32_t lane_off = 4096u * static_cast<uint32_t>(lane >> 4) + 16u * (lane & 15);
-    auto issue_chunk = [&](int c) {
-        const uint32_t kb = lds0 + (c % kDecStages) * kDecStageBytes;
-        const uint32_t vb = kb + kDecKBytes;
-        const int t0 = tok_begin + c * kDecChunk;
-        const bool clamp = t0 + kDecChunk > tok_end;
+    const uint32_t wave_lds = lds0 + static_cast<uint32_t>(wave) * kDecWaveBytes;
+    auto issue_sub = [&](int k) {
+        const int t0 = tok_begin + kDecSubTok * (wave + kDecWaves * k);
+        const uint32_t kb = wave_lds + (k % kDecWaveStages) * 2 * kDecSubBytes;
+        const uint32_t vb = kb + kDecSubBytes;
+        const uint16_t* kbase = kh + static_cast<int64_t>(t0) * kHeadDim;
+        const uint16_t* vbase = vh + static_cast<int64_t>(t0) * kHeadDim;
 #pragma unroll
-        for (int r = 0; r < kDecDmaPerWave; ++r) {
-            const int blk = kDecDmaPerWave * wave + r;
-            int64_t row_base = static_cast<int64_t>(t0 + blk) * kHeadDim;
-            uint32_t off = lane_off;
-            if (clamp) {
-                const int tok = min(t0 + blk + 16 * (lane >> 4), tok_end - 1);
-                row_base = static_cast<int64_t>(t0) * kHeadDim;  // tok >= t0: offset stays >= 0
-                off = static_cast<uint32_t>(tok - t0) * 256u + 16u * (lane & 15);
-            }
-            dec_lds_dma16(kh + row_base, off, kb + kDecKBlock * blk);
-            dec_lds_dma16(vh + row_base, off, vb + kDecVBlock * blk);
+        for (int i = 0; i < 4; ++i) {
+            const int tr = 4 * i + (lane >> 4);
+            const int tok = min(t0 + tr, tok_end - 1);  // t0 < tok_end: offset stays >= 0
+            const uint32_t off = static_cast<uint32_t>(tok - t0) * 256u + 16u * ((lane & 15) ^ dec_swz(tr));
+            dec_lds_dma16(kbase, off, kb + 1024u * i);
+            dec_lds_dma16(vbase, off, vb + 1024u * i);
         }
     };
 
@@ -314,29 +320,30 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         }
     }
 #pragma unroll
-    for (int c = 0; c < kDecStages; ++c)
-        if (c < nchunks) issue_chunk(c);
-    // Wave 0's prologue copies are older than its chunk copies (8 per chunk).
+    for (int k = 0; k < kDecWaveStages; ++k)
+        if (k < nk) issue_sub(k);
+    // Wave 0's prologue copies are older than its sub-chunk copies (8 each).
     if (wave == 0) {
-        const int later = min(kDecStages, nchunks);
+        const int later = min(kDecWaveStages, nk);
         if (later >= 4) {
-            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(8 * kDecDmaPerWave));
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(32));
         } else if (later == 3) {
-            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(6 * kDecDmaPerWave));
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(24));
         } else if (later == 2) {
-            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(4 * kDecDmaPerWave));
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(16));
         } else if (later == 1) {
-            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(2 * kDecDmaPerWave));
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(8));
         } else {
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
         }
     }
 
-    // The split holding the new position (fused form) keeps the rotated K row
-    // and the V row in registers and patches them into its LDS chunk.
+    // The split holding the new position (fused form) leaves the rotated K
+    // row in `pro` row G (over the raw one) next to the V row (row G+1); the
+    // wavefront whose sub-chunk holds the position patches both into its
+    // stage once the copy of that sub-chunk has landed.
     const bool owns_new_row = kFused && (tok_end == s_kv) && (tok_begin < tok_end) &&
                               pos_raw < static_cast<uint32_t>(a.max_seq_len);
-    half8_t knew_lo{}, knew_hi{}, vnew_lo{}, vnew_hi{};
     if constexpr (kFused) {
         if (tid < 64) {
             // f32 angle as the reference computes it; sin/cos correctly
@@ -371,15 +378,16 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
                 }
             } else {
                 const unsigned char* vsrc = pro + (G + 1) * 256;
-                knew_lo = ylo;
-                knew_hi = yhi;
-                vnew_lo = *reinterpret_cast<const half8_t*>(vsrc + 16 * lane8);
-                vnew_hi = *reinterpret_cast<const half8_t*>(vsrc + 128 + 16 * lane8);
+                const half8_t vlo = *reinterpret_cast<const half8_t*>(vsrc + 16 * lane8);
+                const half8_t vhi = *reinterpret_cast<const half8_t*>(vsrc + 128 + 16 * lane8);
+                // Each of these 8 lanes overwrites exactly the 32 B it read.
+                *reinterpret_cast<half8_t*>(pro + G * 256 + 16 * lane8) = ylo;
+                *reinterpret_cast<half8_t*>(pro + G * 256 + 128 + 16 * lane8) = yhi;
                 const int64_t slot = (static_cast<int64_t>(kvh) * a.max_seq_len + pos) * kHeadDim;
                 store_half8(a.k_cache_w + slot + 8 * lane8, ylo);
                 store_half8(a.k_cache_w + slot + 64 + 8 * lane8, yhi);
-                store_half8(a.v_cache_w + slot + 8 * lane8, vnew_lo);
-                store_half8(a.v_cache_w + slot + 64 + 8 * lane8, vnew_hi);
+                store_half8(a.v_cache_w + slot + 8 * lane8, vlo);
+                store_half8(a.v_cache_w + slot + 64 + 8 * lane8, vhi);
             }
         }
         lds_barrier();
@@ -396,10 +404,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             qop[c] = (n < G) ? *reinterpret_cast<const half8_t*>(qsrc + n * kHeadDim + 32 * c + 8 * qgrp)
                              : half8_t{};
     }
-    // Chunk and slot of the new position within this split (owner only).
+    // Sub-chunk (wavefront, index) and row of the new position (owner only).
     const int pos_local = static_cast<int>(pos) - tok_begin;
-    const int c_pos = owns_new_row ? pos_local / kDecChunk : -1;
-    const int t_pos = pos_local % kDecChunk;
+    const int sub_pos = owns_new_row ? pos_local / kDecSubTok : -1;
+    const bool wave_owns = owns_new_row && (sub_pos % kDecWaves) == wave;
+    const int k_pos = wave_owns ? sub_pos / kDecWaves : -1;
+    const int tr_pos = pos_local % kDecSubTok;
 
     float m = kNegBig;
     float l = 0.0f;
@@ -407,104 +417,103 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
 #pragma unroll
     for (int db = 0; db < 8; ++db) acc[db] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    // Per-lane LDS read offsets within a stage.  K (A operand): token
-    // 16*wave + n -> block n, row wave; dims 32c + 8*qgrp.  V^T (transposing
-    // read, 16-lane group qgrp): tokens 16*wave + 4*qgrp + j -> block
-    // 4*qgrp + j, row wave; dims 16db + 4(lane%4).
-    const uint32_t k_lane = n * kDecKBlock + wave * 256 + 16 * qgrp;
-    const uint32_t v_lane = (4 * qgrp + (n >> 2)) * kDecVBlock + wave * 256 + 8 * (n & 3);
+    // Per-lane LDS read offsets within a stage (swizzled rows).  K (A operand
+    // of S^T = K Q^T): token row n, global chunk 4cc + qgrp.  V^T (A operand
+    // of O^T += V^T P^T, transposing read; 16-lane group qgrp, lane n): token
+    // row 4qgrp + n/4, dims 16db + 4(n%4), i.e. 16-byte chunk 2db + (n%4)/2,
+    // half 8*(n%2).
+    uint32_t k_off[4], v_off[8];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) k_off[cc] = n * 256 + 16 * ((4 * cc + qgrp) ^ dec_swz(n));
+    {
+        const int tr = 4 * qgrp + (n >> 2);
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+            v_off[db] = kDecSubBytes + tr * 256 + 16 * ((2 * db + ((n & 3) >> 1)) ^ dec_swz(tr)) + 8 * (n & 1);
+    }
 
-    for (int c = 0; c < nchunks; ++c) {
-        if (c >= 1) {
-            // Every wavefront is past chunk c-1, whose stage now takes chunk
-            // c+3 (chunks 0..3 were issued before the loop); the copy goes
-            // out before this wavefront waits for chunk c.
-            lds_barrier();
-            if (c + kDecStages - 1 < nchunks) issue_chunk(c + kDecStages - 1);
-        }
-        // Chunk c has landed once only the copies of the chunks issued after
-        // it (8 per wave each: chunks c+1..c+3 where they exist) are
-        // outstanding.
-        const int younger = min(kDecStages - 1, nchunks - 1 - c);
+    for (int k = 0; k < nk; ++k) {
+        // Sub-chunk k has landed once only the copies of this wavefront's later
+        // sub-chunks (8 each, up to three) are outstanding.
+        const int younger = min(kDecWaveStages - 1, nk - 1 - k);
         if (younger >= 3) {
-            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(6 * kDecDmaPerWave));
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(24));
         } else if (younger == 2) {
-            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(4 * kDecDmaPerWave));
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(16));
         } else if (younger == 1) {
-            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(2 * kDecDmaPerWave));
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(8));
         } else {
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
         }
-        lds_barrier();
-        if (c == c_pos) {
-            // The copy of this chunk read the cache before the new row was
-            // stored; put the new K/V row into its LDS slot.
-            const int row = tid >> 3, lane8 = tid & 7;
-            if (row == G) {
-                unsigned char* kb = lds + (c % kDecStages) * kDecStageBytes;
-                unsigned char* kr = kb + (t_pos & 15) * kDecKBlock + (t_pos >> 4) * 256;
-                unsigned char* vr = kb + kDecKBytes + (t_pos & 15) * kDecVBlock + (t_pos >> 4) * 256;
-                *reinterpret_cast<half8_t*>(kr + 16 * lane8) = knew_lo;
-                *reinterpret_cast<half8_t*>(kr + 128 + 16 * lane8) = knew_hi;
-                *reinterpret_cast<half8_t*>(vr + 16 * lane8) = vnew_lo;
-                *reinterpret_cast<half8_t*>(vr + 128 + 16 * lane8) = vnew_hi;
+        unsigned char* kb = lds + wave * kDecWaveBytes + (k % kDecWaveStages) * 2 * kDecSubBytes;
+        if (k == k_pos) {
+            // The copy read the cache before the new row was stored: lanes
+            // 0-15 put the rotated K row, lanes 16-31 the V row into row
+            // tr_pos (swizzled).  A wavefront's LDS accesses complete in order.
+            if (lane < 32) {
+                const int j = lane & 15;
+                const half8_t x = *reinterpret_cast<const half8_t*>(pro + (G + (lane >> 4)) * 256 + 16 * j);
+                *reinterpret_cast<half8_t*>(kb + (lane >> 4) * kDecSubBytes + tr_pos * 256 +
+                                            16 * (j ^ dec_swz(tr_pos))) = x;
             }
-            lds_barrier();
         }
 
-        const int t = tok_begin + c * kDecChunk + kDecSub * wave;  // this wave's first token
-        if (t < tok_end) {
-            const unsigned char* kb = lds + (c % kDecStages) * kDecStageBytes;
-            const unsigned char* vb = kb + kDecKBytes;
-            // S^T[token, head]: lane holds head n, tokens t + 4qgrp + r.
-            float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
+        // All LDS operands of the sub-chunk first: once they have arrived the
+        // stage takes sub-chunk k+4, so the copy goes out before the MFMA and
+        // softmax chain instead of after it.
+        half8_t ka[4];
+        half4_t va[8];
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                const half8_t ka = *reinterpret_cast<const half8_t*>(kb + k_lane + 64 * cc);
-                s = mfma16x16x32(ka, qop[cc], s);
-            }
-            float mx = kNegBig;
+        for (int cc = 0; cc < 4; ++cc) ka[cc] = *reinterpret_cast<const half8_t*>(kb + k_off[cc]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = t + 4 * qgrp + r;
-                const float x = (tok < tok_end) ? s[r] * a.scale_log2 : kNegBig;
-                s[r] = x;
-                mx = fmaxf(mx, x);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, swap_halves(mx));
-            // Lazy rescale: the running max m moves only when a score exceeds
-            // it by more than kDecRescaleSlack, so p = 2^(s - m) <= 2^8 stays
-            // well inside f16 and the (rare) rescale of acc and l is the only
-            // place they leave the matrix-core registers.
-            if (__any(mx > m + kDecRescaleSlack)) {
-                const float m_new = fmaxf(m, mx);
-                const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-                l *= alpha;
-#pragma unroll
-                for (int db = 0; db < 8; ++db) acc[db] *= alpha;
-                m = m_new;
-            }
-            float psum = 0.0f;
-            half4_t pop;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float p = __builtin_amdgcn_exp2f(s[r] - m);
-                psum += p;
-                pop[r] = static_cast<half_t>(p);
-            }
-            l += psum;
-#pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                const half4_t vop = lds_read_tr16(reinterpret_cast<const half_t*>(vb + v_lane + 32 * db));
-                acc[db] = mfma16x16x16(vop, pop, acc[db]);
-            }
+        for (int db = 0; db < 8; ++db) va[db] = lds_read_tr16(reinterpret_cast<const half_t*>(kb + v_off[db]));
+        if (k + kDecWaveStages < nk) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue_sub(k + kDecWaveStages);
         }
+
+        const int t = tok_begin + kDecSubTok * (wave + kDecWaves * k);  // first token
+        // S^T[token, head]: lane holds head n, tokens t + 4qgrp + r.
+        float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) s = mfma16x16x32(ka[cc], qop[cc], s);
+        float mx = kNegBig;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = t + 4 * qgrp + r;
+            const float x = (tok < tok_end) ? s[r] * a.scale_log2 : kNegBig;
+            s[r] = x;
+            mx = fmaxf(mx, x);
+        }
+        mx = fmaxf(mx, swap_rows16(mx));
+        mx = fmaxf(mx, swap_halves(mx));
+        // Lazy rescale: the running max m moves only when a score exceeds it
+        // by more than kDecRescaleSlack, so p = 2^(s - m) <= 2^8 stays well
+        // inside f16; the (rare) rescale is the only VALU work on acc.
+        if (__any(mx > m + kDecRescaleSlack)) {
+            const float m_new = fmaxf(m, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) acc[db] *= alpha;
+            m = m_new;
+        }
+        float psum = 0.0f;
+        half4_t pop;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float p = __builtin_amdgcn_exp2f(s[r] - m);
+            psum += p;
+            pop[r] = static_cast<half_t>(p);
+        }
+        l += psum;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) acc[db] = mfma16x16x16(va[db], pop, acc[db]);
     }
 
     // Combine the wavefronts: per head M = max m_w, L = sum l_w 2^(m_w-M),
     // O = sum acc_w 2^(m_w-M) / max(L, 1e-8).
-    l += __shfl_xor(l, 16);
+    l += swap_rows16(l);
     l += swap_halves(l);
     lds_barrier();  // stage buffers are reused for the combine
     float* red = reinterpret_cast<float*>(lds) + wave * kDecRedStride;
@@ -592,7 +601,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         // its LSEs as 16-byte vectors, then accumulates with independent
         // LDS reads, keeping an online (max, sum, acc) across chunks.
         constexpr int kMergeRows = 448;
-        static_assert(kMergeRows * 256 + (kMergeRows + 31 * GROUT_MAX_DECODE_GROUP) * 4 <= kDecStages * kDecStageBytes,
+        static_assert(kMergeRows * 256 + (kMergeRows + 31 * GROUT_MAX_DECODE_GROUP) * 4 <= kDecLdsBytes,
                       "merge batch must fit the stages");
         static_assert(GROUT_MAX_DECODE_GROUP * 32 <= 2 * kDecThreads, "two merge items per thread");
         const int NS = a.num_splits;
@@ -894,10 +903,10 @@ extern "C" int32_t grout_attn_decode_pick_splits(int32_t cu_count, int32_t num_k
     if (cu_count <= 0) cu_count = 256;
     if (num_kv_heads <= 0 || block_n <= 0 || max_context <= 0) return 1;
     // One workgroup per CU (each holds ~130 KB of LDS stages) streaming at the
-    // longest context; a split shorter than one 128-token chunk spends more on
+    // longest context; a split shorter than kDecMinSplitTokens spends more on
     // its prologue and the merge than it saves.
     const int64_t tiles = (static_cast<int64_t>(max_context) + block_n - 1) / block_n;
-    const int64_t min_tiles = (kDecChunk + block_n - 1) / block_n;
+    const int64_t min_tiles = (kDecMinSplitTokens + block_n - 1) / block_n;
     int64_t want = (static_cast<int64_t>(cu_count) + num_kv_heads - 1) / num_kv_heads;
     const int64_t cap = (tiles + min_tiles - 1) / min_tiles;
     if (want > cap) want = cap;

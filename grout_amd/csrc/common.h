@@ -69,6 +69,16 @@ __device__ __forceinline__ float swap_halves(float x) {
     return __builtin_bit_cast(float, lane < 32 ? (int)r[1] : (int)r[0]);
 }
 
+// Value of lane l ^ 16: v_permlane16_swap exchanges 16-lane rows 2i and 2i+1
+// between its two operands; with both equal, an odd row's partner arrives in
+// the first result, an even row's in the second.
+__device__ __forceinline__ float swap_rows16(float x) {
+    int xi = __builtin_bit_cast(int, x);
+    auto r = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+    int lane = __lane_id();
+    return __builtin_bit_cast(float, (lane & 16) ? (int)r[0] : (int)r[1]);
+}
+
 // Orders LDS traffic of one wavefront (lanes exchange data through LDS
 // without a workgroup barrier).
 __device__ __forceinline__ void wave_lds_sync() {
