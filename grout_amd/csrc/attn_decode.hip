@@ -34,9 +34,8 @@
 //    position also writes its K/V row to the cache before streaming.  The
 //    last workgroup of a KV head merges the splits, found with a counter;
 //    the partials travel through agent-coherent (sc1) stores and loads so no
-//    L2-wide writeback/invalidate is needed.  When asked to, the workgroup
-//    holding the last position ticket (taken right after the position read)
-//    advances the device position.
+//    L2-wide writeback/invalidate is needed.  When asked to, the merger of
+//    the last KV head to complete advances the device position.
 #include <math.h>
 
 #include "abi_util.h"
@@ -234,19 +233,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     const uint32_t pos = pos_raw < static_cast<uint32_t>(a.max_seq_len) ? pos_raw
                                                                          : a.max_seq_len - 1;
     const int s_kv = static_cast<int>(pos) + 1;
-    // Position advance: each workgroup takes a ticket once its position read
-    // has completed (the asm consumes the loaded value; its memory clobber
-    // keeps the RMW behind it).  The holder of the last ticket knows every
-    // workgroup has read the position and stores position+1 when it ends;
-    // the RMW's latency overlaps the K/V stream instead of the merge.
-    uint32_t ticket = 0xffffffffu;
-    if constexpr (kFused) {
-        if (a.advance_position && tid == 0) {
-            asm volatile("" ::"s"(pos_raw) : "memory");
-            ticket = __hip_atomic_fetch_add(&a.counters[a.num_kv_heads * kDecCounterStride], 1u, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
     const int tiles = (s_kv + a.block_n - 1) / a.block_n;
     const int per = (tiles + a.num_splits - 1) / a.num_splits;
     const int tb = split * per;
@@ -564,18 +550,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     }
 
     if constexpr (kFused) {
-        const uint32_t last_ticket = static_cast<uint32_t>(a.num_splits) * static_cast<uint32_t>(a.num_kv_heads) - 1u;
-        if (a.advance_position && tid == 0 && ticket == last_ticket) {
-            __hip_atomic_store(&a.counters[a.num_kv_heads * kDecCounterStride], 0u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.position_w, pos_raw + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
         // Last workgroup of this KV head merges its splits.  Every partial is
         // complete at the coherence point (sc1 stores, vmcnt(0)) before this
         // workgroup's counter increment; the merging workgroup reads them with
         // sc1 loads after its own increment returned the final count.
         __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
         lds_barrier();
+        uint32_t head_ticket = 0xffffffffu;
         if (tid == 0) {
             const uint32_t prev = __hip_atomic_fetch_add(&a.counters[kvh * kDecCounterStride], 1u, __ATOMIC_RELAXED,
                                                           __HIP_MEMORY_SCOPE_AGENT);
@@ -584,6 +565,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
                 flag = 1;
                 // This head is complete: reset its counter for the next launch.
                 __hip_atomic_store(&a.counters[kvh * kDecCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                // Position advance: every workgroup of every head read the
+                // position before its head increment, so the merger of the
+                // last head to complete may store position+1.  The head count
+                // is only read after the merge; its latency overlaps the
+                // merge's own round trip.
+                if (a.advance_position)
+                    head_ticket = __hip_atomic_fetch_add(&a.counters[a.num_kv_heads * kDecCounterStride], 1u,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             s_flag = flag;
         }
@@ -692,6 +681,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
                 for (int e = 0; e < 4; ++e) h[e] = static_cast<half_t>(acc[k][e] * inv);
                 *reinterpret_cast<half4_t*>(a.out + (static_cast<int64_t>(kvh) * G + g) * kHeadDim + 4 * c) = h;
             }
+        }
+        if (tid == 0 && head_ticket == static_cast<uint32_t>(a.num_kv_heads) - 1u) {
+            __hip_atomic_store(&a.counters[a.num_kv_heads * kDecCounterStride], 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.position_w, pos_raw + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
