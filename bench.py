@@ -13,8 +13,10 @@ fp16 dense MFMA peak, and decode attention GB/s as a fraction of HBM peak.
   also    = c3's fused QK norm/RoPE/KV write (HBM-bound) and c2 (Qwen3-4B
             decode at context 4096).
 
-Kernel durations come from HIP events recorded on the launch stream around
-each launch.  The CPU baseline is the oracle (a C port of the reference's fp32
+Kernel durations come from HIP events recorded on the launch stream: around
+each launch for prefill, and around a run of back-to-back launches (divided by
+the count) for the microsecond-scale decode and norm kernels, whose per-launch
+event pairs would add the launch latency.  The CPU baseline is the oracle (a C port of the reference's fp32
 CPU attention, benchmarks/src/bin/attention_microbench.rs:665-702) run on a
 bounded row sample of the same inputs.
 
@@ -33,14 +35,21 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# HIP runtime setting for the decode-graph replays, read when HIP initialises
+# (so before torch is imported): with the runtime's graph packet capture on, each
+# replay of the one-kernel decode graph costs ~4 us more GPU time than the same
+# kernel launched directly (measured 34.0 vs 30.2 us per step); with it off a
+# replay costs what a launch costs.  An explicit setting in the environment wins.
+GRAPH_PACKET_CAPTURE = os.environ.setdefault("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0")
+
 METRIC = ("prefill attn TFLOP/s (% fp16 MFMA peak); decode attn GB/s (% HBM peak), 1 GPU")
 PEAK_TFLOPS_F16 = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz (dense fp16 MFMA)
 PEAK_HBM_GBS = 8000.0      # HBM3E
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0), the
 # scales read off a 1 GiB copy; the runs and figures are in profiles/*.txt.
 PMC_TRAFFIC_BYTES = {
-    "attn_prefill_c3": (71373.6 * 2.0 + 65732.7) * 1024,
-    "attn_decode_fused_c4": (66019.3 * 2.0 + 2108.5) * 1024,
+    "attn_prefill_c3": (71782.8 * 2.0 + 65536.0) * 1024,
+    "attn_decode_fused_c4": (65984.5 * 2.0 + 2108.3) * 1024,
 }
 D = 128
 EPS = 1e-6
@@ -87,6 +96,22 @@ def time_launches(torch, fn, steps: int, warmup: int, stream=None):
     return durs, wall
 
 
+def time_back_to_back(torch, fn, n: int, warmup: int, stream=None) -> float:
+    """Average duration (ms) of n launches issued back to back between two events."""
+    s = stream or torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(s)
+    for _ in range(n):
+        fn()
+    b.record(s)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n
+
+
 def bench_prefill(torch, ga, steps, warmup, gen):
     hq, hkv, S = 32, 8, 8192
     q = torch.randn((S, hq, D), device="cuda", generator=gen, dtype=torch.float32).half()
@@ -115,8 +140,7 @@ def bench_norm(torch, ga, steps, warmup, gen):
     vc = torch.zeros_like(kc)
     out = torch.empty_like(q)
     fn = lambda: ga.qk_norm_rope_kv_prefill(q, k, v, qw, kw, inv, out, kc, vc, EPS, 0)  # noqa
-    durs, _ = time_launches(torch, fn, steps, warmup)
-    ms = sum(durs) / len(durs)
+    ms = time_back_to_back(torch, fn, max(steps, 50), warmup)
     nb = norm_bytes(hq, hkv, S)
     return dict(ms=ms, bytes=nb, gbs=nb / (ms * 1e-3) / 1e9)
 
@@ -164,22 +188,22 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
     avg_bytes = sum(decode_bytes(hq, hkv, ctx + i + 1) for i in range(replays)) / replays
 
     # The fused step alone (the graph's only kernel), eager at position ctx
-    # (s_kv = ctx + 1, position not advanced), per-launch events; then the
+    # (s_kv = ctx + 1, position not advanced), back-to-back launches; then the
     # standalone split and merge ops of the same shape.
     counters = ga.decode_counters(hkv)
     pos_t.fill_(ctx)
     with torch.cuda.stream(s):
         ffn = lambda: ga.decode_fused(qkv, qw, kw, inv, q_out, kc, vc, att, lse, attn_out,  # noqa
                                       counters, pos_t, EPS, scale_bits, hq, hkv)
-        fdurs, _ = time_launches(torch, ffn, split_steps, 10, stream=s)
+        fused_us = 1e3 * time_back_to_back(torch, ffn, split_steps, 10, stream=s)
         q_grouped = q_out[:hq].view(hkv, G, D)
         fn = lambda: ga.fmha_decode_gqa_split(q_grouped, kc, vc, att, lse, scale_bits, pos_t)  # noqa
-        durs, _ = time_launches(torch, fn, split_steps, 10, stream=s)
+        split_us = 1e3 * time_back_to_back(torch, fn, split_steps, 10, stream=s)
         mfn = lambda: ga.splitk_reduce_merge(att, lse, attn_out)  # noqa: E731
+        # A ~4 us kernel launched back to back through the Python mirror is
+        # host-bound; per-launch event pairs bound it from above instead.
         mdurs, _ = time_launches(torch, mfn, split_steps, 10, stream=s)
-    fused_us = 1e3 * sum(fdurs) / len(fdurs)
-    split_us = 1e3 * sum(durs) / len(durs)
-    merge_us = 1e3 * sum(mdurs) / len(mdurs)
+        merge_us = 1e3 * sum(mdurs) / len(mdurs)
     bytes_step = decode_bytes(hq, hkv, ctx + 1)
     return dict(
         hq=hq, hkv=hkv, ctx=ctx, num_splits=ns, replays=replays, step_us=step_us,
@@ -344,6 +368,7 @@ def main(argv=None) -> int:
             "roofline": rl("hbm", dec["fused_gbs"], PEAK_HBM_GBS, "GB/s",
                            traffic=round(PMC_TRAFFIC_BYTES["attn_decode_fused_c4"])),
             "step_frac_of_hbm_peak": round(dec["step_gbs"] / PEAK_HBM_GBS, 4),
+            "hip_graph_packet_capture": GRAPH_PACKET_CAPTURE,
             "cpu_baseline": cpu_dec,
         },
         "decode_c2": {"us_per_step": round(dec2["step_us"], 3),
