@@ -15,23 +15,25 @@
 // Decode is HBM-bound (4-8 FLOP per byte); the kernel is shaped for bytes in
 // flight:
 //  * Workgroup = (split, kv_head), 4 wavefronts, one per CU (LDS-bound).
-//    The split's tokens stream through LDS in 64-token chunks (K 16 KB +
-//    V 16 KB) with direct HBM->LDS copies over 4 stages: after the one
-//    barrier per chunk the next-but-two chunk is issued, so ~96-128 KB per
-//    CU are in flight while a chunk is computed, without staging registers.
-//  * Each wavefront takes 16 tokens of a chunk.  All G query heads of the KV
-//    head share every K/V byte: S^T = K Q^T runs on v_mfma_f32_16x16x32_f16
-//    and O^T += V^T P^T on v_mfma_f32_16x16x16_f16 with the G heads (padded to
-//    16) as N.  The S^T accumulator layout is exactly the P^T operand
-//    (reduction slot j of lane group q is token 4q+j); V^T is read in the same
-//    order with one ds_read_b64_tr_b16 per 16 dims.
-//  * LDS rows are interleaved (token t in block t%16, row t/16) with padded
-//    block strides, so the operand reads are bank-conflict free and every
-//    read address is a per-lane base plus an immediate.
+//    Each wavefront streams its own 16-token sub-chunks of the split (K 4 KB +
+//    V 4 KB each) through a private 4-stage LDS ring with direct HBM->LDS
+//    copies; it waits only for its own copies, so the stream has no
+//    workgroup barrier, and the next copy goes out as soon as the operands
+//    of the current sub-chunk have been read.
+//  * All G query heads of the KV head share every K/V byte: S^T = K Q^T runs
+//    on v_mfma_f32_16x16x32_f16 and O^T += V^T P^T on v_mfma_f32_16x16x16_f16
+//    with the G heads (padded to 16) as N.  The S^T accumulator layout is
+//    exactly the P^T operand (reduction slot j of lane group q is token
+//    4q+j); V^T is read in the same order with one ds_read_b64_tr_b16 per 16
+//    dims.
+//  * Token rows sit unpadded in LDS with their 16-byte chunks XOR-swizzled
+//    by the copy itself (each lane fetches the chunk that belongs at its
+//    destination), so the K and V^T operand reads are bank-conflict free.
 //  * The four wavefronts' (m, l, acc) are combined through LDS at the end.
 //  * Fused form: every workgroup recomputes its G query rows (RMSNorm +
 //    RoPE, as the prefill/decode norm kernel); the split holding the new
-//    position also writes its K/V row to the cache before streaming.  The
+//    position also writes its K/V row to the cache and patches it into the
+//    sub-chunk whose copy read the cache before that store.  The
 //    last workgroup of a KV head merges the splits, found with a counter;
 //    the partials travel through agent-coherent (sc1) stores and loads so no
 //    L2-wide writeback/invalidate is needed.  When asked to, the merger of
