@@ -1,0 +1,127 @@
+"""GPU parity at the benchmark configurations' full shapes.
+
+* c3: Qwen3-4B causal prefill, S=8192, 32 Q / 8 KV heads; the fp32 oracle on a
+  stride sample of query rows (all heads).
+* c5: Qwen3-32B causal prefill, S=32768, 64 Q / 8 KV heads, 1% of K rows x8
+  (online-softmax rescale stress), then 64 decode steps appending to the same
+  KV cache through the hipGraph runner (fused norm/RoPE/KV write + split-K +
+  merge); every step is checked against the oracle's norm/RoPE/KV write and
+  its split/merge restatement.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import (D, EPS, THETA, assert_close_attn, f16_ulp_diff, normal_f16,
+                         norm_weight, qk_scale_f16_bits, rng)
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 1.0 / math.sqrt(D)
+BN = 32
+
+
+def _prefill(torch, q, kc, vc, query_start=0):
+    import grout_amd
+
+    dq = torch.from_numpy(q).cuda()
+    dk = torch.from_numpy(kc).cuda()
+    dv = torch.from_numpy(vc).cuda()
+    out = torch.empty_like(dq)
+    grout_amd.attend_prefill(dq, dk, dv, out, query_start)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), dk, dv
+
+
+def _row_ref(q, kc, vc, r, kv_len):
+    """fp32 oracle for query row r alone (position r, keys 0..r)."""
+    return oracle.attn_prefill_f32(np.ascontiguousarray(q[r:r + 1]), kc, vc, SCALE,
+                                   kv_len=kv_len, query_start=r)[0]
+
+
+def test_c3_prefill_sampled_rows(gpu):
+    import torch
+
+    g = rng(300)
+    S, hq, hkv = 8192, 32, 8
+    q = normal_f16(g, (S, hq, D))
+    kc = normal_f16(g, (hkv, S, D))
+    vc = normal_f16(g, (hkv, S, D))
+    out, _, _ = _prefill(torch, q, kc, vc)
+    rows = np.concatenate([np.arange(5, S, 127), [S - 1]])
+    ref = np.stack([_row_ref(q, kc, vc, int(r), S) for r in rows])
+    assert_close_attn(out[rows], ref, "c3 prefill sampled rows")
+
+
+def test_c5_prefill_then_64_decode_steps(gpu):
+    import torch
+
+    import grout_amd
+
+    g = rng(301)
+    S, hq, hkv, steps = 32768, 64, 8, 64
+    G = hq // hkv
+    MS = S + steps
+    q = normal_f16(g, (S, hq, D))
+    kc = np.zeros((hkv, MS, D), dtype=np.float16)
+    vc = np.zeros((hkv, MS, D), dtype=np.float16)
+    kc[:, :S] = normal_f16(g, (hkv, S, D))
+    vc[:, :S] = normal_f16(g, (hkv, S, D))
+    outlier = g.random((hkv, S)) < 0.01
+    kc[:, :S][outlier] = (kc[:, :S][outlier].astype(np.float32) * 8).astype(np.float16)
+
+    out, dkc, dvc = _prefill(torch, q, kc, vc)
+    assert np.isfinite(out).all()
+    rows = np.concatenate([np.arange(11, S, 1021), [S - 1]])
+    ref = np.stack([_row_ref(q, kc, vc, int(r), S) for r in rows])
+    assert_close_attn(out[rows], ref, "c5 prefill sampled rows")
+    del q, out, ref
+
+    # 64 decode steps at positions S..S+63 on the same device caches.
+    qw, kw = norm_weight(g), norm_weight(g)
+    inv = oracle.build_inv_freq(THETA)
+    ns = grout_amd.pick_num_splits(MS, hkv)
+    dev = dict(
+        qkv=torch.zeros(((hq + 2 * hkv) * D,), dtype=torch.float16, device="cuda"),
+        q_weight=torch.from_numpy(qw).cuda(), k_weight=torch.from_numpy(kw).cuda(),
+        inv_freq=torch.from_numpy(inv).cuda(),
+        q_out=torch.zeros(((hq + hkv), D), dtype=torch.float16, device="cuda"),
+        k_cache=dkc, v_cache=dvc,
+        attn_out=torch.zeros((hkv, G, D), dtype=torch.float16, device="cuda"),
+        position=torch.zeros((1,), dtype=torch.int32, device="cuda"),
+    )
+    att, lse = grout_amd.decode_scratch(hkv, G, ns)
+    # The prime pass runs one step at S before capture: give it the first step's
+    # inputs so the cache slot it writes is rewritten identically by replay 0.
+    qkvs = [normal_f16(g, ((hq + 2 * hkv) * D,)) for _ in range(steps)]
+    dev["qkv"].copy_(torch.from_numpy(qkvs[0]).cuda())
+    runner = grout_amd.DecodeGraphRunner(
+        **dev, att_partial=att, lse_partial=lse, eps=EPS,
+        qk_scale_f16_bits=qk_scale_f16_bits(), num_q_heads=hq, num_kv_heads=hkv,
+        num_splits=ns, prime_position=S)
+    kc_ref, vc_ref = kc, vc
+    try:
+        for step in range(steps):
+            pos = S + step
+            with torch.cuda.stream(runner.stream):
+                dev["qkv"].copy_(torch.from_numpy(qkvs[step]).cuda())
+                runner.launch_step(pos)
+            runner.stream.synchronize()
+            got = dev["attn_out"].cpu().numpy()
+            qo_ref = np.zeros(((hq + hkv), D), dtype=np.float16)
+            oracle.qk_norm_rope_kv_decode(qkvs[step], qw, kw, inv, qo_ref, kc_ref, vc_ref, pos,
+                                          EPS, hq, hkv)
+            qg = np.ascontiguousarray(qo_ref[:hq].reshape(hkv, G, D))
+            a_ref, l_ref = oracle.attn_decode_split(qg, kc_ref, vc_ref, qk_scale_f16_bits(), pos,
+                                                    BN, ns)
+            assert_close_attn(got, oracle.attn_decode_merge(a_ref, l_ref, G),
+                              f"c5 decode step {step} (position {pos})")
+        assert int(dev["position"].item()) == S + steps
+        kc_dev = dkc[:, S:].cpu().numpy()
+        vc_dev = dvc[:, S:].cpu().numpy()
+        assert f16_ulp_diff(kc_dev, kc_ref[:, S:]).max() <= 1
+        assert np.array_equal(vc_dev.view(np.uint16), vc_ref[:, S:].view(np.uint16))
+    finally:
+        runner.close()
