@@ -45,13 +45,13 @@ namespace grout {
 
 constexpr int kPfBN = 64;     // keys per tile
 // LDS tile layout: key row n of a tile sits in 1 KB block n%16 at row n/16
-// (256 B rows inside a block); blocks are 1040 B (K) / 1056 B (V) apart.
+// (256 B rows inside a block); blocks are 1040 B (K) / 1088 B (V) apart.
 // One direct-to-LDS copy fills one block (rows b, b+16, b+32, b+48), the
 // MFMA operand reads (8 or 16 consecutive keys, or 4 keys x 32 B for the
 // transposing V reads) hit distinct banks, and every read address is a
 // per-lane base plus an immediate offset.
 constexpr int kPfKBlock = 1040;
-constexpr int kPfVBlock = 1056;
+constexpr int kPfVBlock = 1088;
 constexpr int kPfKBytes = 16 * kPfKBlock;
 constexpr int kPfVBytes = 16 * kPfVBlock;
 constexpr int kPfStageBytes = kPfKBytes + kPfVBytes;
