@@ -292,6 +292,12 @@ class DecodeGraphRunner:
     def launch_step(self, position: int):
         _check(lib().grout_decode_runner_step(self._h, int(position)), "decode_runner_step")
 
+    def run(self, first_position: int, count: int):
+        """`count` consecutive steps from `first_position`, issued from C without
+        returning to Python between steps (the graph advances the position)."""
+        _check(lib().grout_decode_runner_run(self._h, int(first_position), int(count)),
+               "decode_runner_run")
+
     def zero_kv_caches(self):
         _check(lib().grout_decode_runner_zero_kv(self._h), "decode_runner_zero_kv")
 

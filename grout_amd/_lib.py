@@ -74,6 +74,7 @@ SIGNATURES = {
     "grout_decode_runner_create": (
         c_i32, [ctypes.POINTER(DecodeLayer), c_u32, c_vp, ctypes.POINTER(c_vp)]),
     "grout_decode_runner_step": (c_i32, [c_vp, c_u32]),
+    "grout_decode_runner_run": (c_i32, [c_vp, c_u32, c_i32]),
     "grout_decode_runner_zero_kv": (c_i32, [c_vp]),
     "grout_decode_runner_destroy": (c_i32, [c_vp]),
 }

@@ -197,6 +197,25 @@ extern "C" int32_t grout_decode_runner_step(grout_decode_runner* runner, uint32_
     return st;
 }
 
+extern "C" int32_t grout_decode_runner_run(grout_decode_runner* runner, uint32_t first_position,
+                                           int32_t count) {
+    GROUT_REQUIRE(runner != nullptr && runner->graph != nullptr, GROUT_ERR_GRAPH);
+    GROUT_REQUIRE(count >= 0, GROUT_ERR_ARG);
+    if (count == 0) return GROUT_OK;
+    GROUT_REQUIRE(static_cast<uint64_t>(first_position) + static_cast<uint64_t>(count) <=
+                      static_cast<uint64_t>(runner->layer.max_seq_len),
+                  GROUT_ERR_SEQ_RANGE);
+    // The first step positions the graph; every replay advances the device
+    // position itself, so the following replays need no host write.
+    int32_t st = grout_decode_runner_step(runner, first_position);
+    grout_stream_t gs = reinterpret_cast<grout_stream_t>(runner->stream);
+    for (int32_t i = 1; st == GROUT_OK && i < count; ++i) {
+        st = grout_graph_launch(runner->graph, gs);
+        if (st == GROUT_OK) runner->next_position = first_position + static_cast<uint32_t>(i) + 1;
+    }
+    return st;
+}
+
 extern "C" int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner) {
     GROUT_REQUIRE(runner != nullptr, GROUT_ERR_GRAPH);
     const grout_decode_layer& L = runner->layer;

@@ -251,6 +251,13 @@ int32_t grout_decode_runner_create(const grout_decode_layer* layer, uint32_t pri
  * (a stream-ordered write unless the previous step already left it there),
  * replay the graph.  No host sync. */
 int32_t grout_decode_runner_step(grout_decode_runner* runner, uint32_t position);
+/* `count` consecutive steps at positions first_position .. first_position+count-1
+ * without returning to the caller in between: launch_step (src/model.rs:363-403)
+ * repeated, for a decode loop whose per-token state stays on the device (the
+ * reference's graph writes the sampled token in place).  Only the first step
+ * may write the position; the graph advances it for the others.  No host sync. */
+int32_t grout_decode_runner_run(grout_decode_runner* runner, uint32_t first_position,
+                                int32_t count);
 /* zero_kv_caches (src/model.rs:433-462): clear both caches in place; pointers
  * stay valid for the captured graph.  Synchronises the runner's stream. */
 int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner);

@@ -150,6 +150,7 @@ def test_graph_handle_checks(L):
     assert L.grout_graph_destroy(None) == 0
     assert L.grout_set_position_async(None, 3, None) == -1
     assert L.grout_decode_runner_step(None, 0) == -10
+    assert L.grout_decode_runner_run(None, 0, 4) == -10
     assert L.grout_decode_runner_destroy(None) == 0
 
 

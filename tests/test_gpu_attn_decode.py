@@ -175,6 +175,23 @@ def test_graph_runner_replay(gpu):
         # The prime pass wrote slot p0 once before capture; the replays rewrote it.
         assert int(dev["position"].item()) == p0 + 9
         assert int(runner.counters.abs().sum().item()) == 0
+        # run(): four consecutive steps issued from C with one qkv; equals four
+        # oracle steps on the same input.
+        qkv = normal_f16(g, ((hq + 2 * hkv) * D,))
+        with torch.cuda.stream(runner.stream):
+            dev["qkv"].copy_(torch.from_numpy(qkv).cuda())
+            runner.run(p0 + 20, 4)
+        runner.stream.synchronize()
+        for pos in range(p0 + 20, p0 + 24):
+            qo_ref = np.zeros(((hq + hkv), D), dtype=np.float16)
+            oracle.qk_norm_rope_kv_decode(qkv, qw, kw, inv, qo_ref, kc_ref, vc_ref, pos, EPS,
+                                          hq, hkv)
+        qg = np.ascontiguousarray(qo_ref[:hq].reshape(hkv, G, D))
+        a_ref, l_ref = oracle.attn_decode_split(qg, kc_ref, vc_ref, qk_scale_f16_bits(),
+                                                p0 + 23, BN, ns)
+        assert_close_attn(dev["attn_out"].cpu().numpy(), oracle.attn_decode_merge(a_ref, l_ref, G),
+                          "run x4")
+        assert int(dev["position"].item()) == p0 + 24
         kc_dev = dev["k_cache"].cpu().numpy()
         from tests._util import f16_ulp_diff
         assert f16_ulp_diff(kc_dev, kc_ref).max() <= 1
