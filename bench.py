@@ -145,6 +145,26 @@ def bench_norm(torch, ga, steps, warmup, gen):
     return dict(ms=ms, bytes=nb, gbs=nb / (ms * 1e-3) / 1e9)
 
 
+def bench_kv_update(torch, ga, steps, warmup, gen):
+    """kv_cache_update_seq at c3 shapes: 8192 rows x 8 KV heads of K and V into
+    a [8, 8192, 128] cache (read 33.6 MB, write 33.6 MB)."""
+    hkv, S = 8, 8192
+    nk = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
+    nv = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
+    kc = torch.zeros((hkv, S, D), device="cuda", dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    ga.kv_cache_update_seq(nk, nv, kc, vc, 0)  # argument checks of the Python mirror once
+    # Back to back through the C entry point: the ~12 us kernel outruns the
+    # Python mirror's per-call cost.
+    L = ga.lib()
+    args = (nk.data_ptr(), nv.data_ptr(), kc.data_ptr(), vc.data_ptr(), 0, S, hkv, D, S,
+            torch.cuda.current_stream().cuda_stream)
+    fn = lambda: L.grout_kv_cache_update_seq(*args)  # noqa: E731
+    ms = time_back_to_back(torch, fn, max(steps, 50), warmup)
+    nb = 2 * 2 * S * hkv * D * 2
+    return dict(ms=ms, bytes=nb, gbs=nb / (ms * 1e-3) / 1e9)
+
+
 def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
     """Graph replay of {norm/RoPE/KV write, split, merge} at positions ctx..ctx+replays-1,
     plus event-timed eager launches of the split kernel alone at position ctx."""
@@ -256,7 +276,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "norm"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "norm", "kv"], default="all",
                     help="run one workload only (for profiling runs); prints no JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (reads and writes 1 GiB) "
@@ -298,6 +318,9 @@ def main(argv=None) -> int:
         elif args.only == "norm":
             nrm = bench_norm(torch, ga, args.steps, args.warmup, gen)
             log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
+        elif args.only == "kv":
+            kvu = bench_kv_update(torch, ga, args.steps, args.warmup, gen)
+            log(f"kv update c3: {kvu['ms'] * 1e3:.1f} us, {kvu['gbs']:.0f} GB/s")
         else:
             dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, args.warmup, gen,
                                args.steps)
@@ -311,6 +334,8 @@ def main(argv=None) -> int:
     log("qk_norm_rope c3 ...")
     nrm = bench_norm(torch, ga, args.steps, args.warmup, gen)
     log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
+    kvu = bench_kv_update(torch, ga, args.steps, args.warmup, gen)
+    log(f"kv update c3: {kvu['ms'] * 1e3:.1f} us, {kvu['gbs']:.0f} GB/s")
     log("decode c4 ...")
     dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, 20, gen, 200)
     log(f"decode c4: graph step {dec['step_us']:.2f} us ({dec['step_gbs']:.0f} GB/s), "
@@ -376,6 +401,8 @@ def main(argv=None) -> int:
                       "num_splits": dec2["num_splits"]},
         "qk_norm_rope_c3": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                             "frac_of_hbm_peak": round(nrm["gbs"] / PEAK_HBM_GBS, 4)},
+        "kv_cache_update_c3": {"us": round(kvu["ms"] * 1e3, 2), "GB/s": round(kvu["gbs"], 1),
+                               "frac_of_hbm_peak": round(kvu["gbs"] / PEAK_HBM_GBS, 4)},
     }
     print(json.dumps(line), flush=True)
     return 0

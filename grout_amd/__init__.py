@@ -135,6 +135,49 @@ def qk_norm_rope_kv_prefill(q, k, v, q_weight, k_weight, inv_freq, out, k_cache,
     return out
 
 
+def _kv_update_checks(new_k, new_v, k_cache, v_cache):
+    """The shape ensure!s of kv_cache_update_seq_arc_ctx_with_position
+    (src/model.rs:5396-5423); returns (S, Hkv, D, MS)."""
+    _ensure(new_k.dim() == 3,
+            f"new_k must be rank 3 [seqlen, kv_heads, head_dim], got {list(new_k.shape)}")
+    S, Hkv, D = new_k.shape
+    _ensure(k_cache.dim() == 3 and k_cache.shape[0] == Hkv and k_cache.shape[2] == D,
+            f"new_k shape mismatch: {list(new_k.shape)}")
+    _ensure(list(new_v.shape) == [S, Hkv, D], f"new_v shape mismatch: {list(new_v.shape)}")
+    MS = k_cache.shape[1]
+    _ensure(list(v_cache.shape) == [Hkv, MS, D],
+            f"v_cache shape mismatch: {list(v_cache.shape)}")
+    for t, n in ((new_k, "new_k"), (new_v, "new_v"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _f16(t, n)
+    return S, Hkv, D, MS
+
+
+def kv_cache_update_seq(new_k, new_v, k_cache, v_cache, position_start: int):
+    """kv_cache_update_seq_arc_ctx_with_position with a host position
+    (src/model.rs:5388-5480, kv_cache_update_seq_f16): cache rows
+    [position_start, position_start+S) of every KV head take new_k/new_v."""
+    S, Hkv, D, MS = _kv_update_checks(new_k, new_v, k_cache, v_cache)
+    _ensure(position_start + S <= MS,
+            f"kv_cache_update range [{position_start}..{position_start + S}) exceeds "
+            f"max_seq_len {MS}")
+    _check(lib().grout_kv_cache_update_seq(
+        _ptr(new_k), _ptr(new_v), _ptr(k_cache), _ptr(v_cache), int(position_start), S, Hkv, D,
+        MS, _stream()), "kv_cache_update_seq")
+
+
+def kv_cache_update_seq_dynpos(new_k, new_v, k_cache, v_cache, position):
+    """The device-position form (src/model.rs:5433-5441, 5483-5502,
+    kv_cache_update_seq_dynpos_f16): ``position`` is a device u32 tensor of
+    shape [1]; the decode-graph path writes one row."""
+    S, Hkv, D, MS = _kv_update_checks(new_k, new_v, k_cache, v_cache)
+    _ensure(S == 1, f"decode graph path expects seq_len=1, got {S}")
+    _ensure(list(position.shape) == [1],
+            f"kv_cache position tensor must be shape [1], got {list(position.shape)}")
+    _check(lib().grout_kv_cache_update_seq_dynpos(
+        _ptr(new_k), _ptr(new_v), _ptr(k_cache), _ptr(v_cache), _ptr(position), S, Hkv, D, MS,
+        _stream()), "kv_cache_update_seq_dynpos")
+
+
 def qk_norm_rope_kv_decode(qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache,
                            position, eps: float, num_q_heads: int, num_kv_heads: int):
     """qk_norm_rope_kv_decode_raw_f16 as recorded at src/model.rs:3194-3221.

@@ -73,6 +73,8 @@ SIGNATURES = {
     "grout_set_position_async": (c_i32, [c_vp, c_u32, c_vp]),
     "grout_decode_runner_create": (
         c_i32, [ctypes.POINTER(DecodeLayer), c_u32, c_vp, ctypes.POINTER(c_vp)]),
+    "grout_kv_cache_update_seq": (c_i32, [c_vp] * 4 + [c_i32] * 5 + [c_vp]),
+    "grout_kv_cache_update_seq_dynpos": (c_i32, [c_vp] * 5 + [c_i32] * 4 + [c_vp]),
     "grout_decode_runner_step": (c_i32, [c_vp, c_u32]),
     "grout_decode_runner_run": (c_i32, [c_vp, c_u32, c_i32]),
     "grout_decode_runner_zero_kv": (c_i32, [c_vp]),

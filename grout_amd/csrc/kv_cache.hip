@@ -1,0 +1,122 @@
+// Unfused KV-cache suffix writer: rows [position_start, position_start+seq_len)
+// of every KV head's cache take new_k/new_v, bit for bit.
+//
+// Replaces kv_cache_update_seq_f16 (src/kernels.rs:759-800, host position,
+// launched at src/model.rs:5464-5480 for chunked prefill and MTP suffixes) and
+// kv_cache_update_seq_dynpos_f16 (src/kernels.rs:807-846, device position,
+// the graph-captured decode path at src/model.rs:5483-5502).
+//   new_k/new_v [seq_len, num_kv_heads, head_dim] f16, contiguous;
+//   k_cache/v_cache [num_kv_heads, max_seq_len, head_dim] f16.
+// HBM-bound copy: every thread moves one 16-byte (or, for head_dim % 8 != 0,
+// 8-byte) unit of K and the same unit of V; consecutive threads read
+// consecutive source bytes and write within one cache row.
+#include "abi_util.h"
+#include "common.h"
+
+namespace grout {
+
+template <typename Unit, bool kDevicePos>
+__global__ __launch_bounds__(256) void kv_cache_update_kernel(
+    const Unit* __restrict__ new_k, const Unit* __restrict__ new_v, Unit* __restrict__ k_cache,
+    Unit* __restrict__ v_cache, int position_start, const uint32_t* __restrict__ d_position,
+    int64_t total_units, int units_per_row, int num_kv_heads, int max_seq_len) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= total_units) return;
+    const int u = static_cast<int>(i % units_per_row);
+    const int64_t rh = i / units_per_row;  // = s * num_kv_heads + h
+    const int h = static_cast<int>(rh % num_kv_heads);
+    const int64_t s = rh / num_kv_heads;
+    int64_t pos;
+    if constexpr (kDevicePos) {
+        pos = static_cast<int64_t>(*d_position) + s;
+        if (pos >= max_seq_len) return;  // bounds guard: a slot past the cache is not written
+    } else {
+        pos = position_start + s;
+    }
+    const int64_t dst = (static_cast<int64_t>(h) * max_seq_len + pos) * units_per_row + u;
+    k_cache[dst] = new_k[i];
+    v_cache[dst] = new_v[i];
+}
+
+template <bool kDevicePos>
+static int32_t launch_kv_update(const uint16_t* new_k, const uint16_t* new_v, uint16_t* k_cache,
+                                uint16_t* v_cache, int32_t position_start,
+                                const uint32_t* d_position, int32_t seq_len,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                                hipStream_t stream) {
+    const bool wide = head_dim % 8 == 0;
+    const int units_per_row = wide ? head_dim / 8 : head_dim / 4;
+    const int64_t total = static_cast<int64_t>(seq_len) * num_kv_heads * units_per_row;
+    if (total == 0) return GROUT_OK;
+    const int64_t blocks = (total + 255) / 256;
+    if (blocks > 0x7fffffff) return GROUT_ERR_SEQ_RANGE;
+    if (wide) {
+        hipLaunchKernelGGL((kv_cache_update_kernel<uint4_t, kDevicePos>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(256), 0, stream, reinterpret_cast<const uint4_t*>(new_k),
+                           reinterpret_cast<const uint4_t*>(new_v), reinterpret_cast<uint4_t*>(k_cache),
+                           reinterpret_cast<uint4_t*>(v_cache), position_start, d_position, total,
+                           units_per_row, num_kv_heads, max_seq_len);
+    } else {
+        typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+        hipLaunchKernelGGL((kv_cache_update_kernel<uint2_t, kDevicePos>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(256), 0, stream, reinterpret_cast<const uint2_t*>(new_k),
+                           reinterpret_cast<const uint2_t*>(new_v), reinterpret_cast<uint2_t*>(k_cache),
+                           reinterpret_cast<uint2_t*>(v_cache), position_start, d_position, total,
+                           units_per_row, num_kv_heads, max_seq_len);
+    }
+    return launch_status();
+}
+
+// Shared checks of both entry points (the shape ensure!s of
+// kv_cache_update_seq_arc_ctx_with_position, src/model.rs:5396-5423, on sizes).
+static int32_t check_kv_update(const uint16_t* new_k, const uint16_t* new_v, uint16_t* k_cache,
+                               uint16_t* v_cache, int32_t seq_len, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t max_seq_len) {
+    GROUT_REQUIRE(new_k != nullptr && new_v != nullptr && k_cache != nullptr && v_cache != nullptr,
+                  GROUT_ERR_NULL_POINTER);
+    // head_dim is free here (grout's engine uses 128); rows move in 8- or
+    // 16-byte units, so it must be a multiple of 4.
+    GROUT_REQUIRE(head_dim > 0 && head_dim % 4 == 0, GROUT_ERR_HEAD_DIM);
+    GROUT_REQUIRE(num_kv_heads > 0, GROUT_ERR_HEADS);
+    GROUT_REQUIRE(max_seq_len > 0 && seq_len >= 0, GROUT_ERR_SEQ_RANGE);
+    const uintptr_t align = head_dim % 8 == 0 ? 15u : 7u;
+    GROUT_REQUIRE(((reinterpret_cast<uintptr_t>(new_k) | reinterpret_cast<uintptr_t>(new_v) |
+                    reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) &
+                   align) == 0,
+                  GROUT_ERR_ALIGNMENT);
+    return GROUT_OK;
+}
+
+}  // namespace grout
+
+using namespace grout;
+
+extern "C" int32_t grout_kv_cache_update_seq(const uint16_t* new_k, const uint16_t* new_v,
+                                             uint16_t* k_cache, uint16_t* v_cache,
+                                             int32_t position_start, int32_t seq_len,
+                                             int32_t num_kv_heads, int32_t head_dim,
+                                             int32_t max_seq_len, grout_stream_t stream) {
+    const int32_t st = check_kv_update(new_k, new_v, k_cache, v_cache, seq_len, num_kv_heads,
+                                       head_dim, max_seq_len);
+    if (st != GROUT_OK) return st;
+    // src/model.rs:5425-5431: position_start + seq_len <= max_seq_len.
+    GROUT_REQUIRE(position_start >= 0 &&
+                      static_cast<int64_t>(position_start) + seq_len <= max_seq_len,
+                  GROUT_ERR_SEQ_RANGE);
+    return launch_kv_update<false>(new_k, new_v, k_cache, v_cache, position_start, nullptr,
+                                   seq_len, num_kv_heads, head_dim, max_seq_len, to_hip(stream));
+}
+
+extern "C" int32_t grout_kv_cache_update_seq_dynpos(const uint16_t* new_k, const uint16_t* new_v,
+                                                    uint16_t* k_cache, uint16_t* v_cache,
+                                                    const uint32_t* d_position, int32_t seq_len,
+                                                    int32_t num_kv_heads, int32_t head_dim,
+                                                    int32_t max_seq_len, grout_stream_t stream) {
+    GROUT_REQUIRE(d_position != nullptr, GROUT_ERR_NULL_POINTER);
+    GROUT_REQUIRE((reinterpret_cast<uintptr_t>(d_position) & 3u) == 0, GROUT_ERR_ALIGNMENT);
+    const int32_t st = check_kv_update(new_k, new_v, k_cache, v_cache, seq_len, num_kv_heads,
+                                       head_dim, max_seq_len);
+    if (st != GROUT_OK) return st;
+    return launch_kv_update<true>(new_k, new_v, k_cache, v_cache, 0, d_position, seq_len,
+                                  num_kv_heads, head_dim, max_seq_len, to_hip(stream));
+}

@@ -103,6 +103,29 @@ int32_t grout_qk_norm_rope_kv_decode(const uint16_t* qkv, const uint16_t* q_weig
                                      int32_t head_dim, int32_t max_seq_len,
                                      grout_stream_t stream);
 
+/* ------------------------------------------------- KV-cache suffix writer */
+/* Replaces kv_cache_update_seq_f16 (src/kernels.rs:759-800) as launched by
+ * kv_cache_update_seq_arc_ctx_with_position (src/model.rs:5464-5480): the
+ * unfused KV write of chunked prefill and MTP suffixes.
+ *   new_k/new_v [seq_len, num_kv_heads, head_dim] f16; cache rows
+ *   [position_start, position_start+seq_len) of k_cache/v_cache
+ *   [num_kv_heads, max_seq_len, head_dim] take them bit-exactly; every other
+ *   row is untouched.  head_dim is any multiple of 4 (grout uses 128);
+ *   pointers 16-byte aligned (8-byte when head_dim % 8 != 0). */
+int32_t grout_kv_cache_update_seq(const uint16_t* new_k, const uint16_t* new_v,
+                                  uint16_t* k_cache, uint16_t* v_cache, int32_t position_start,
+                                  int32_t seq_len, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t max_seq_len, grout_stream_t stream);
+/* Replaces kv_cache_update_seq_dynpos_f16 (src/kernels.rs:807-846), the
+ * graph-captured form (src/model.rs:5483-5502): the start slot is the device
+ * u32 *d_position.  A row whose slot falls at or past max_seq_len is not
+ * written (bounds guard). */
+int32_t grout_kv_cache_update_seq_dynpos(const uint16_t* new_k, const uint16_t* new_v,
+                                         uint16_t* k_cache, uint16_t* v_cache,
+                                         const uint32_t* d_position, int32_t seq_len,
+                                         int32_t num_kv_heads, int32_t head_dim,
+                                         int32_t max_seq_len, grout_stream_t stream);
+
 /* ------------------------------------------ causal prefill attention (A4-A7) */
 /* Replaces fmha_prefill_causal / fmha_prefill_gqa / fmha_prefill_gqa_lpt /
  * flash_attn_causal_seq_f16 (src/kernels.rs:1037-1862) as dispatched by

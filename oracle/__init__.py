@@ -57,6 +57,7 @@ def lib():
             [_u16p] * 4 + [_f32p, ctypes.c_uint16, ctypes.c_uint32] + [_i32] * 7)
         L.go_attn_decode_merge.argtypes = [_u16p, _f32p, _u16p] + [_i32] * 4
         L.go_decode_split_range.argtypes = [_i32] * 4 + [ctypes.POINTER(_i32)] * 2
+        L.go_kv_cache_update_seq.argtypes = [_u16p] * 4 + [_i32] * 5
         _lib = L
     return _lib
 
@@ -163,3 +164,10 @@ def decode_split_range(s_kv: int, block_n: int, num_splits: int, split: int):
     lib().go_decode_split_range(s_kv, block_n, num_splits, split, ctypes.byref(b),
                                 ctypes.byref(e))
     return b.value, e.value
+
+
+def kv_cache_update_seq(new_k, new_v, k_cache, v_cache, position_start: int):
+    """Writes cache rows [position_start, position_start+S) in place."""
+    S, Hkv, D = new_k.shape
+    lib().go_kv_cache_update_seq(_u16(new_k), _u16(new_v), _u16(k_cache), _u16(v_cache),
+                                 position_start, S, Hkv, D, k_cache.shape[1])

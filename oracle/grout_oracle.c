@@ -422,3 +422,23 @@ void go_attn_decode_merge(const uint16_t* att_partial, const float* lse_partial,
     }
     free(w);
 }
+
+/* src/kernels.rs:759-800 kv_cache_update_seq_f16: each cache tile owns absolute
+ * slots s_global and takes input row s_global - position_start when
+ * position_start <= s_global < position_start + seq_len (:783-797). */
+void go_kv_cache_update_seq(const uint16_t* new_k, const uint16_t* new_v, uint16_t* k_cache,
+                            uint16_t* v_cache, int32_t position_start, int32_t seq_len,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t max_seq) {
+    for (int32_t h = 0; h < num_kv_heads; ++h) {
+        for (int32_t s_global = 0; s_global < max_seq; ++s_global) {
+            if (s_global < position_start || s_global >= position_start + seq_len) continue;
+            const int64_t row = s_global - position_start;
+            const int64_t src = (row * num_kv_heads + h) * head_dim;
+            const int64_t dst = ((int64_t)h * max_seq + s_global) * head_dim;
+            for (int32_t d = 0; d < head_dim; ++d) {
+                k_cache[dst + d] = new_k[src + d];
+                v_cache[dst + d] = new_v[src + d];
+            }
+        }
+    }
+}

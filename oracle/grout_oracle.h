@@ -78,6 +78,13 @@ void go_attn_decode_merge(const uint16_t* att_partial, const float* lse_partial,
 void go_decode_split_range(int32_t s_kv, int32_t block_n, int32_t num_splits, int32_t split,
                            int32_t* tile_begin, int32_t* tile_end);
 
+/* src/kernels.rs:759-800 kv_cache_update_seq_f16: cache slot
+ * [h, position_start + r, :] = new[r, h, :] for r < seq_len (every other slot
+ * untouched); new [seq_len, Hkv, D], caches [Hkv, max_seq, D]. */
+void go_kv_cache_update_seq(const uint16_t* new_k, const uint16_t* new_v, uint16_t* k_cache,
+                            uint16_t* v_cache, int32_t position_start, int32_t seq_len,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t max_seq);
+
 #ifdef __cplusplus
 }
 #endif

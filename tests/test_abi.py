@@ -144,6 +144,21 @@ def test_decode_fused_checks(L):
     assert call(12, -1.0) == -9                           # eps
 
 
+def test_kv_cache_update_checks(L):
+    f = L.grout_kv_cache_update_seq
+    # new_k, new_v, k_cache, v_cache, start, S, Hkv, D, MS, stream
+    assert f(0, A, A, A, 0, 4, 2, 128, 16, S) == -1
+    assert f(A, A, A, A, 0, 4, 2, 126, 16, S) == -3       # head_dim not a multiple of 4
+    assert f(A, A, A, A, 0, 4, 0, 128, 16, S) == -4
+    assert f(A, A, A, A, 13, 4, 2, 128, 16, S) == -5      # 17 > max_seq_len
+    assert f(A, A, A, A, -1, 4, 2, 128, 16, S) == -5
+    assert f(A + 8, A, A, A, 0, 4, 2, 128, 16, S) == -2   # 8-byte aligned, 16-byte rows
+    assert f(A, A, A, A, 0, 0, 2, 128, 16, S) == 0        # empty: nothing launched
+    g = L.grout_kv_cache_update_seq_dynpos
+    assert g(A, A, A, A, 0, 1, 2, 128, 16, S) == -1
+    assert g(A, A, A, A, A + 2, 1, 2, 128, 16, S) == -2
+
+
 def test_graph_handle_checks(L):
     assert L.grout_graph_begin(None) == -10
     assert L.grout_graph_launch(None, None) == -10

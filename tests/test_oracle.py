@@ -311,3 +311,36 @@ def test_decode_scale_is_f16_rounded():
     """src/model.rs:3427: the decode scale is f16(1/sqrt(128)) = 0.08837890625."""
     assert qk_scale_f16_bits() == 0x2DA8 == oracle.f16_bits(SCALE)
     assert float(np.array([0x2DA8], np.uint16).view(np.float16)[0]) == 0.08837890625
+
+
+def test_kv_cache_update_seq_reference_kat():
+    """tests/kernels.rs:67-118 (mtp_kv_suffix_write_preserves_prefix_and_unused_tail):
+    HEADS=2, CAPACITY=16, D=4, ROWS=5, START=3, incoming values i+1; slot
+    [h, pos, d] = values[((pos-START)*HEADS + h)*D + d] inside the range, the
+    zero-initialised prefix and tail stay 0."""
+    HEADS, CAP, D, ROWS, START = 2, 16, 4, 5, 3
+    values = (np.arange(ROWS * HEADS * D) + 1).astype(np.float16).reshape(ROWS, HEADS, D)
+    k = np.zeros((HEADS, CAP, D), np.float16)
+    v = np.zeros((HEADS, CAP, D), np.float16)
+    oracle.kv_cache_update_seq(values, values, k, v, START)
+    flat = values.reshape(-1)
+    for h in range(HEADS):
+        for pos in range(CAP):
+            for d in range(D):
+                exp = flat[((pos - START) * HEADS + h) * D + d] if START <= pos < START + ROWS else 0
+                assert k[h, pos, d] == exp and v[h, pos, d] == exp
+
+
+def test_kv_cache_update_seq_leaves_other_slots():
+    """Rows outside [start, start+S) keep whatever the cache held (sentinels)."""
+    g = np.random.default_rng(5)
+    Hkv, MS, D, S, start = 3, 40, 128, 7, 29
+    nk = g.standard_normal((S, Hkv, D)).astype(np.float16)
+    nv = g.standard_normal((S, Hkv, D)).astype(np.float16)
+    k = np.full((Hkv, MS, D), 7.0, np.float16)
+    v = np.full((Hkv, MS, D), -3.0, np.float16)
+    oracle.kv_cache_update_seq(nk, nv, k, v, start)
+    assert np.array_equal(k[:, start:start + S], nk.transpose(1, 0, 2))
+    assert np.array_equal(v[:, start:start + S], nv.transpose(1, 0, 2))
+    assert (k[:, :start] == 7).all() and (k[:, start + S:] == 7).all()
+    assert (v[:, :start] == -3).all() and (v[:, start + S:] == -3).all()
