@@ -62,7 +62,11 @@ constexpr int kDecMinSplitTokens = 64;
 // one row per lane) and, for the transposing V reads, spreading each 32-lane
 // half over all 64 banks.
 __device__ __forceinline__ int dec_swz(int tr) { return 2 * (tr & 7) + (tr >> 3); }
-constexpr int kDecRedStride = 16 * kHeadDim + 32;   // floats per wave in the final combine
+// Final combine of the wavefronts: per wave 16 head rows of kHeadDim + 4
+// floats (the pad puts the 16 rows a lane group writes in distinct banks),
+// then m and l of the 16 heads.
+constexpr int kDecRedRow = kHeadDim + 4;
+constexpr int kDecRedStride = 16 * kDecRedRow + 32;   // floats per wave
 constexpr float kNegBig = -1.0e30f;
 // Lazy rescale slack of the decode softmax (log2 units): p <= 2^8.
 constexpr float kDecRescaleSlack = 8.0f;
@@ -506,13 +510,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     lds_barrier();  // stage buffers are reused for the combine
     float* red = reinterpret_cast<float*>(lds) + wave * kDecRedStride;
     if (qgrp == 0) {
-        red[16 * kHeadDim + n] = m;
-        red[16 * kHeadDim + 16 + n] = l;
+        red[16 * kDecRedRow + n] = m;
+        red[16 * kDecRedRow + 16 + n] = l;
     }
 #pragma unroll
     for (int db = 0; db < 8; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[n * kHeadDim + 16 * db + 4 * qgrp + r] = acc[db][r];
+        *reinterpret_cast<float4_t*>(red + n * kDecRedRow + 16 * db + 4 * qgrp) = acc[db];
     lds_barrier();
 
     {
@@ -522,21 +525,22 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             const float* base = reinterpret_cast<const float*>(lds);
             float M = kNegBig;
 #pragma unroll
-            for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, base[w * kDecRedStride + 16 * kHeadDim + g]);
+            for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, base[w * kDecRedStride + 16 * kDecRedRow + g]);
             float L = 0.0f, f[kDecWaves];
 #pragma unroll
             for (int w = 0; w < kDecWaves; ++w) {
-                f[w] = exp2f(base[w * kDecRedStride + 16 * kHeadDim + g] - M);
-                L += base[w * kDecRedStride + 16 * kHeadDim + 16 + g] * f[w];
+                f[w] = __builtin_amdgcn_exp2f(base[w * kDecRedStride + 16 * kDecRedRow + g] - M);
+                L += base[w * kDecRedStride + 16 * kDecRedRow + 16 + g] * f[w];
             }
             const float l_safe = fmaxf(L, 1.0e-8f);
+            const float inv_l = 1.0f / l_safe;
             half8_t o;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float x = 0.0f;
 #pragma unroll
-                for (int w = 0; w < kDecWaves; ++w) x += base[w * kDecRedStride + g * kHeadDim + d0 + e] * f[w];
-                o[e] = static_cast<half_t>(x / l_safe);
+                for (int w = 0; w < kDecWaves; ++w) x += base[w * kDecRedStride + g * kDecRedRow + d0 + e] * f[w];
+                o[e] = static_cast<half_t>(x * inv_l);
             }
             const int64_t prow = (static_cast<int64_t>(kvh) * a.num_splits + split) * G + g;
             const float lse_v = M + log2f(l_safe);
