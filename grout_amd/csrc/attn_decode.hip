@@ -203,14 +203,14 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Agent-coherent (sc1) 16-byte store / load as four relaxed agent-scope
-// 32-bit atomics: visible to a workgroup on another XCD without an L2-wide
-// writeback or invalidate.
+// Agent-coherent 16-byte store: one global_store_dwordx4 with the sc1 cache
+// policy, the form a relaxed agent-scope atomic store takes on this target,
+// so a workgroup on another XCD sees it without an L2-wide writeback or
+// invalidate.  The kernel orders it with s_waitcnt vmcnt(0) before the
+// counter increment that publishes it.
 __device__ __forceinline__ void store16_agent(uint16_t* p, half8_t v) {
     const uint4_t u = __builtin_bit_cast(uint4_t, v);
-    uint32_t* q = reinterpret_cast<uint32_t*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) __hip_atomic_store(q + i, u[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(u) : "memory");
 }
 
 __device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t c) {
