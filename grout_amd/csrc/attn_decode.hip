@@ -236,6 +236,41 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
 
     // Position from device memory; reads are clamped to the cache.
     const uint32_t pos_raw = *a.d_position;
+    // Prologue inputs into `pro` (wave 0).  None depends on the position, so
+    // the copies go out while the position load is in flight; the K/V
+    // sub-chunk copies follow once the split range is known.
+    const uint32_t pro0 = static_cast<uint32_t>(
+        (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(pro)));
+    const int n_pro = kFused ? G + 5 : G;
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < kDecProDmas; ++i) {
+            if (4 * i < n_pro) {
+                int r = 4 * i + (lane >> 4);
+                if (r >= n_pro) r = 0;  // pad lanes repeat row 0
+                const unsigned char* src;
+                if constexpr (kFused) {
+                    const int64_t hq = a.num_q_heads, hkv = a.num_kv_heads;
+                    if (r < G) {
+                        src = reinterpret_cast<const unsigned char*>(a.qkv + (static_cast<int64_t>(kvh) * G + r) * kHeadDim);
+                    } else if (r == G) {
+                        src = reinterpret_cast<const unsigned char*>(a.qkv + (hq + kvh) * kHeadDim);
+                    } else if (r == G + 1) {
+                        src = reinterpret_cast<const unsigned char*>(a.qkv + (hq + hkv + kvh) * kHeadDim);
+                    } else if (r == G + 2) {
+                        src = reinterpret_cast<const unsigned char*>(a.q_weight);
+                    } else if (r == G + 3) {
+                        src = reinterpret_cast<const unsigned char*>(a.k_weight);
+                    } else {
+                        src = reinterpret_cast<const unsigned char*>(a.inv_freq);
+                    }
+                } else {
+                    src = reinterpret_cast<const unsigned char*>(a.q + (static_cast<int64_t>(kvh) * G + r) * kHeadDim);
+                }
+                dec_lds_dma16_ptr(src + 16 * (lane & 15), pro0 + 1024u * i);
+            }
+        }
+    }
     const uint32_t pos = pos_raw < static_cast<uint32_t>(a.max_seq_len) ? pos_raw
                                                                          : a.max_seq_len - 1;
     const int s_kv = static_cast<int>(pos) + 1;
@@ -277,40 +312,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         }
     };
 
-    // Prologue inputs into `pro` (wave 0), then the first K/V chunks (all
-    // waves); nothing waits on an ordinary load, so the copies go out at once.
-    const uint32_t pro0 = static_cast<uint32_t>(
-        (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(pro)));
-    const int n_pro = kFused ? G + 5 : G;
-    if (wave == 0) {
-#pragma unroll
-        for (int i = 0; i < kDecProDmas; ++i) {
-            if (4 * i < n_pro) {
-                int r = 4 * i + (lane >> 4);
-                if (r >= n_pro) r = 0;  // pad lanes repeat row 0
-                const unsigned char* src;
-                if constexpr (kFused) {
-                    const int64_t hq = a.num_q_heads, hkv = a.num_kv_heads;
-                    if (r < G) {
-                        src = reinterpret_cast<const unsigned char*>(a.qkv + (static_cast<int64_t>(kvh) * G + r) * kHeadDim);
-                    } else if (r == G) {
-                        src = reinterpret_cast<const unsigned char*>(a.qkv + (hq + kvh) * kHeadDim);
-                    } else if (r == G + 1) {
-                        src = reinterpret_cast<const unsigned char*>(a.qkv + (hq + hkv + kvh) * kHeadDim);
-                    } else if (r == G + 2) {
-                        src = reinterpret_cast<const unsigned char*>(a.q_weight);
-                    } else if (r == G + 3) {
-                        src = reinterpret_cast<const unsigned char*>(a.k_weight);
-                    } else {
-                        src = reinterpret_cast<const unsigned char*>(a.inv_freq);
-                    }
-                } else {
-                    src = reinterpret_cast<const unsigned char*>(a.q + (static_cast<int64_t>(kvh) * G + r) * kHeadDim);
-                }
-                dec_lds_dma16_ptr(src + 16 * (lane & 15), pro0 + 1024u * i);
-            }
-        }
-    }
 #pragma unroll
     for (int k = 0; k < kDecWaveStages; ++k)
         if (k < nk) issue_sub(k);
