@@ -48,8 +48,8 @@ PEAK_HBM_GBS = 8000.0      # HBM3E
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0), the
 # scales read off a 1 GiB copy; the runs and figures are in profiles/*.txt.
 PMC_TRAFFIC_BYTES = {
-    "attn_prefill_c3": (71782.8 * 2.0 + 65536.0) * 1024,
-    "attn_decode_fused_c4": (65984.5 * 2.0 + 2108.3) * 1024,
+    "attn_prefill_c3": (71767.0 * 2.0 + 65536.0) * 1024,
+    "attn_decode_fused_c4": (65976.8 * 2.0 + 572.3) * 1024,
 }
 D = 128
 EPS = 1e-6
@@ -273,7 +273,9 @@ def main(argv=None) -> int:
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 50 warmup launches (~30 ms of prefill) bring the clocks up from idle;
+    # with 5 the first timed launches still run ramping up.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "prefill", "decode", "norm", "kv"], default="all",
