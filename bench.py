@@ -232,6 +232,43 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
         kc=kc, vc=vc, q=q_out[:hq].clone())
 
 
+def bench_mfma_probe(torch, launches: int = 8):
+    """Sustained v_mfma_f32_32x32x16_f16 rate for operands distributed like the
+    prefill kernel's (grout_amd/probe/mfma_ceiling.hip): mode 0 = both N(0,1)
+    (Q K^T), mode 1 = N(0,1) x [0,1) (P V).  Returns TFLOP/s per mode and the
+    rate of an equal mix of the two (harmonic mean: equal MFMA counts)."""
+    import ctypes
+
+    from grout_amd import build as gbuild
+
+    if not os.path.exists(gbuild.PROBE_LIB_PATH):
+        raise RuntimeError(f"{gbuild.PROBE_LIB_PATH} is not built; run `python -m grout_amd.build`")
+    lib = ctypes.CDLL(gbuild.PROBE_LIB_PATH)
+    fn = lib.grout_probe_mfma_f16
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
+                   ctypes.c_void_p]
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 4000
+    out = torch.empty((blocks * 512,), device="cuda", dtype=torch.float32)
+    stream = torch.cuda.current_stream()
+    res = {}
+    for mode in (0, 1):
+        for i in range(3):
+            assert fn(out.data_ptr(), blocks, iters, mode, i, stream.cuda_stream) == 0
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(launches):
+            assert fn(out.data_ptr(), blocks, iters, mode, 100 + i, stream.cuda_stream) == 0
+        b.record(stream)
+        torch.cuda.synchronize()
+        flops = launches * blocks * 8.0 * iters * 16 * 32768
+        res[mode] = flops / (a.elapsed_time(b) * 1e-3) / 1e12
+    mix = 2.0 / (1.0 / res[0] + 1.0 / res[1])
+    return dict(qk=res[0], pv=res[1], mix=mix, blocks=blocks)
+
+
 def cpu_baseline_prefill(torch, pre, threads: int):
     """Oracle fp32 attention over every query row of the c3 inputs (about 10 s on 16 cores)."""
     import oracle
@@ -278,7 +315,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "norm", "kv"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "norm", "kv", "mfma-probe"],
+                    default="all",
                     help="run one workload only (for profiling runs); prints no JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (reads and writes 1 GiB) "
@@ -323,6 +361,10 @@ def main(argv=None) -> int:
         elif args.only == "kv":
             kvu = bench_kv_update(torch, ga, args.steps, args.warmup, gen)
             log(f"kv update c3: {kvu['ms'] * 1e3:.1f} us, {kvu['gbs']:.0f} GB/s")
+        elif args.only == "mfma-probe":
+            mp = bench_mfma_probe(torch)
+            log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
+                f"mix {mp['mix']:.0f} TFLOP/s")
         else:
             dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, args.warmup, gen,
                                args.steps)
@@ -333,6 +375,10 @@ def main(argv=None) -> int:
     log("prefill c3 ...")
     pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
     log(f"prefill c3: {pre['ms']:.3f} ms/launch, {pre['tflops']:.1f} TFLOP/s")
+    log("mfma probe ...")
+    mp = bench_mfma_probe(torch)
+    log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
+        f"mix {mp['mix']:.0f} TFLOP/s; prefill = {pre['tflops'] / mp['mix']:.3f} of the mix")
     log("qk_norm_rope c3 ...")
     nrm = bench_norm(torch, ga, args.steps, args.warmup, gen)
     log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
@@ -382,6 +428,13 @@ def main(argv=None) -> int:
         "roofline": rl("mfma", pre["tflops"], PEAK_TFLOPS_F16, "TFLOP/s",
                        traffic=round(PMC_TRAFFIC_BYTES["attn_prefill_c3"])),
         "cpu_baseline": cpu,
+        # What the matrix cores sustain on this GPU for operands distributed like
+        # the prefill kernel's (MFMAs only, no memory or softmax work).
+        "mfma_ceiling_probe": {
+            "unit": "TFLOP/s", "qk_operands": round(mp["qk"], 1), "pv_operands": round(mp["pv"], 1),
+            "mix": round(mp["mix"], 1), "frac_of_nominal_peak": round(mp["mix"] / PEAK_TFLOPS_F16, 4),
+            "prefill_frac_of_mix": round(pre["tflops"] / mp["mix"], 4),
+            "source": "grout_amd/probe/mfma_ceiling.hip"},
         "decode": {
             "workload": "c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context 32768, "
                         f"hipGraph x{dec['replays']} of the fused step (norm/RoPE/KV write + "

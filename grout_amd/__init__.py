@@ -38,7 +38,8 @@ from ._lib import GROUT_OK, LibraryMissing
 __all__ = [
     "GroutError", "LibraryMissing", "lib", "build_inv_freq", "qk_norm_rope_kv_prefill",
     "qk_norm_rope_kv_decode", "attend_prefill", "fmha_decode_gqa_split",
-    "splitk_reduce_merge", "decode_fused", "decode_scratch", "decode_counters",
+    "splitk_reduce_merge", "decode_fused", "attend_prefill_split", "prefill_split_scratch",
+    "prefill_splitk_reduce_merge", "decode_scratch", "decode_counters",
     "pick_num_splits", "DecodeGraphRunner",
     "HEAD_DIM", "ATTN_BN_DECODE",
 ]
@@ -216,6 +217,63 @@ def attend_prefill(q, k_cache, v_cache, out, position_start: int,
     _check(lib().grout_attn_prefill(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), float(qk_scale), Hq, Hkv, D, q_len,
         int(kv_len), int(position_start), MS, _stream()), "attn_prefill")
+    return out
+
+
+def prefill_split_scratch(num_q_heads: int, q_len: int, block_m: int, group: int,
+                          num_splits: int, head_dim: int = HEAD_DIM, device="cuda"):
+    """Scratch of fmha_prefill_gqa_lpt_split (src/kernels.rs:1922-1944):
+    att [tiles, NKS*BM*group, D] f16, lse [tiles, NKS*BM*group] f32 with
+    tiles = ceil(q_len/BM) * (Hq/group)."""
+    torch = _torch()
+    rows = lib().grout_attn_prefill_split_lse_bytes(num_q_heads, q_len, block_m, group,
+                                                    num_splits)
+    _ensure(rows >= 0, "invalid split-K prefill geometry")
+    rows //= 4
+    ns_m = num_splits * block_m * group
+    att = torch.zeros((rows // ns_m, ns_m, head_dim), dtype=torch.float16, device=device)
+    lse = torch.zeros((rows // ns_m, ns_m), dtype=torch.float32, device=device)
+    return att, lse
+
+
+def attend_prefill_split(q, k_cache, v_cache, att_partial, lse_partial, position_start: int,
+                         block_m: int, block_n: int, group: int, num_splits: int,
+                         qk_scale: float | None = None, kv_len: int | None = None):
+    """fmha_prefill_gqa_lpt_split (src/kernels.rs:1872-2142) as the attention
+    microbench launches it (benchmarks/src/bin/attention_microbench.rs:411-469),
+    on grout's cache layout; writes the normalised per-split partials and LSEs."""
+    _ensure(q.dim() == 3, f"q must be rank 3 [seqlen, heads, head_dim], got {list(q.shape)}")
+    q_len, Hq, D = q.shape
+    Hkv, MS, _ = k_cache.shape
+    qgs = Hq // Hkv if Hkv else 0
+    _ensure(group >= 1 and qgs % group == 0, f"group must divide q_group_size={qgs}")
+    if qk_scale is None:
+        qk_scale = 1.0 / math.sqrt(float(D))
+    if kv_len is None:
+        kv_len = position_start + q_len
+    ns_m = num_splits * block_m * group
+    tiles = -(-q_len // block_m) * (Hq // group)
+    _ensure(list(att_partial.shape) == [tiles, ns_m, D],
+            f"att_partial shape mismatch, got {list(att_partial.shape)}")
+    _ensure(list(lse_partial.shape) == [tiles, ns_m],
+            f"lse_partial shape mismatch, got {list(lse_partial.shape)}")
+    for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache"),
+                 (att_partial, "att_partial")):
+        _f16(t, n)
+    _check(lib().grout_attn_prefill_split(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(att_partial), _ptr(lse_partial),
+        float(qk_scale), Hq, Hkv, D, q_len, int(kv_len), int(position_start), MS, block_m,
+        block_n, group, num_splits, _stream()), "fmha_prefill_gqa_lpt_split")
+
+
+def prefill_splitk_reduce_merge(att_partial, lse_partial, out, block_m: int, group: int,
+                                num_splits: int):
+    """prefill_splitk_reduce_merge (src/kernels.rs:2151-2323); out [q_len, Hq, D]."""
+    q_len, Hq, D = out.shape
+    _f16(out, "out")
+    _check(lib().grout_attn_prefill_split_merge(
+        _ptr(att_partial), _ptr(lse_partial), _ptr(out), Hq, D, q_len, block_m, group,
+        num_splits, _stream()), "prefill_splitk_reduce_merge")
     return out
 
 

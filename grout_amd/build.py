@@ -2,6 +2,9 @@
 
 Usage: ``python -m grout_amd.build [--verbose]``.  Each ``csrc/*.hip`` file is
 compiled separately (in parallel) and linked into ``grout_amd/libgrout_attn_hip.so``.
+The measurement probe ``probe/*.hip`` (an MFMA-rate calibration bench.py
+reports beside the prefill roofline; not part of the C ABI) is linked into
+``grout_amd/libgrout_probe.so``.
 """
 from __future__ import annotations
 
@@ -17,6 +20,8 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libgrout_attn_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
+PROBE_DIR = os.path.join(HERE, "probe")
+PROBE_LIB_PATH = os.path.join(HERE, "libgrout_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -43,8 +48,8 @@ HIP_FLAGS = [
 ]
 
 
-def sources() -> list[str]:
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+def sources(d: str = CSRC) -> list[str]:
+    return sorted(os.path.join(d, f) for f in os.listdir(d) if f.endswith(".hip"))
 
 
 def _compile(src: str, verbose: bool, extra: list[str]) -> str:
@@ -62,21 +67,27 @@ def _compile(src: str, verbose: bool, extra: list[str]) -> str:
     return obj
 
 
-def build(verbose: bool = False, extra: list[str] | None = None) -> str:
-    """Compile every csrc/*.hip for gfx950 and link the shared library."""
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    extra = list(extra or [])
-    srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=min(len(srcs), 8)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose, extra), srcs))
-    tmp = LIB_PATH + ".tmp"
+def _link(objs: list[str], path: str, verbose: bool) -> None:
+    tmp = path + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build(verbose: bool = False, extra: list[str] | None = None) -> str:
+    """Compile every csrc/*.hip (and probe/*.hip) for gfx950 and link the libraries."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    extra = list(extra or [])
+    srcs = sources()
+    probe_srcs = sources(PROBE_DIR)
+    with cf.ThreadPoolExecutor(max_workers=min(len(srcs) + len(probe_srcs), 8)) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose, extra), srcs + probe_srcs))
+    _link(objs[:len(srcs)], LIB_PATH, verbose)
+    _link(objs[len(srcs):], PROBE_LIB_PATH, verbose)
     return LIB_PATH
 
 

@@ -76,9 +76,16 @@ struct PrefillArgs {
     int kv_len;
     int query_start;
     int max_seq_len;
-    int n_pos_tiles;       // ceil(q_len / rows per wavefront)
+    int n_pos_tiles;       // ceil(q_len / rows per wavefront) (split: padded to whole q blocks)
     int tasks_per_head;    // n_pos_tiles * group wavefront tasks per KV head
     int blocks_per_head;   // ceil(tasks_per_head / waves per workgroup)
+    // Split-K form only (fmha_prefill_gqa_lpt_split's generics and scratch).
+    uint16_t* att_partial;  // [tiles, num_splits*block_m*split_group, 128]
+    float* lse_partial;     // [tiles, num_splits*block_m*split_group]
+    int block_m;            // BM: query rows per q block (a multiple of 32)
+    int block_n;            // BN: keys per split-range tile
+    int split_group;        // GROUP: q heads per logical tile
+    int num_splits;
 };
 
 // Asynchronous 16-byte HBM -> LDS copy (global_load_lds_dwordx4, scalar base
@@ -120,6 +127,12 @@ __device__ __forceinline__ void pf_barrier() {
 constexpr int kPfWaves = 8;
 constexpr int kPfRows = 32;
 
+// kSplit: the split-K form (fmha_prefill_gqa_lpt_split, src/kernels.rs:1872-2142).
+// Workgroup (task, blockIdx.y = split); every wavefront restricts its keys to
+// its split's range, computed from the reference's q block of its rows
+// (block_m is a multiple of 32, so a wavefront's rows lie in one block), and
+// stores a normalised partial and its log2 LSE instead of the output.
+template <bool kSplit>
 __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(PrefillArgs a) {
     constexpr int kDmaPerWave = 16 / kPfWaves;  // K blocks (and V blocks) per wavefront
     __shared__ __attribute__((aligned(1024))) unsigned char pf_lds[kPfStages * kPfStageBytes];
@@ -149,9 +162,39 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
 
     const int pt_max = a.n_pos_tiles - 1 - (rblk * kPfWaves) / a.group;
     const int blk_kv_end = min(a.kv_len, a.query_start + pt_max * kPfRows + kPfRows);
-    const int ntiles = (blk_kv_end + kPfBN - 1) / kPfBN;
-    const int wave_kv_end = task_ok ? min(a.kv_len, pos0 + kPfRows) : 0;
-    const int wave_tiles = (wave_kv_end + kPfBN - 1) / kPfBN;
+    int wave_kv_end = task_ok ? min(a.kv_len, pos0 + kPfRows) : 0;
+    // Key range [lo, hi) of this wavefront (all keys unless split) and the
+    // workgroup's range of 64-key tiles [tile0, tile0 + ntiles).
+    int key_lo = 0, key_hi = a.kv_len, tile0 = 0, blk_end = blk_kv_end;
+    if constexpr (kSplit) {
+        // src/kernels.rs:2036-2043 for q block bq: tc = ceil(min(m_end, kv_len)/BN),
+        // tps = ceil(tc/NKS), split s covers tiles [s*tps, min(s*tps+tps, tc)).
+        auto split_range = [&](int bq, int& lo, int& hi) {
+            const int m_end = a.query_start + (bq + 1) * a.block_m;
+            const int tc = (min(m_end, a.kv_len) + a.block_n - 1) / a.block_n;
+            const int tps = (tc + a.num_splits - 1) / a.num_splits;
+            const int st = static_cast<int>(blockIdx.y) * tps;
+            const int et = min(st + tps, tc);
+            lo = st * a.block_n;
+            hi = max(lo, min(et * a.block_n, a.kv_len));
+        };
+        split_range(row0 / a.block_m, key_lo, key_hi);
+        wave_kv_end = min(wave_kv_end, key_hi);
+        if (wave_kv_end <= key_lo) wave_kv_end = 0;  // empty range: no tile
+        // The ranges grow with the q block, so the workgroup's union runs from
+        // its lowest block's start to its highest block's end.
+        const int pt_min = max(0, a.n_pos_tiles - 1 - (rblk * kPfWaves + kPfWaves - 1) / a.group);
+        int lo_min, hi_min, lo_max, hi_max;
+        split_range(pt_min * kPfRows / a.block_m, lo_min, hi_min);
+        split_range(pt_max * kPfRows / a.block_m, lo_max, hi_max);
+        blk_end = min(blk_kv_end, hi_max);
+        tile0 = lo_min / kPfBN;
+        if (blk_end <= lo_min) blk_end = tile0 * kPfBN;  // no key in any range
+    }
+    const int ntiles = max(0, (blk_end + kPfBN - 1) / kPfBN - tile0);
+    // This wavefront's active tiles [wave_t0, wave_tiles), relative to tile0.
+    const int wave_t0 = (wave_kv_end > 0) ? key_lo / kPfBN - tile0 : 0;
+    const int wave_tiles = (wave_kv_end > 0) ? (wave_kv_end + kPfBN - 1) / kPfBN - tile0 : 0;
 
     const uint16_t* kh = a.k_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
     const uint16_t* vh = a.v_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
@@ -166,7 +209,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     auto issue_tile = [&](int tile, int st) {
         const uint32_t kb = lds0 + st * kPfStageBytes;
         const uint32_t vb = kb + kPfKBytes;
-        const int n0 = tile * kPfBN;
+        const int n0 = (tile0 + tile) * kPfBN;
         const bool clamp = n0 + kPfBN > blk_kv_end;
 #pragma unroll
         for (int r = 0; r < kDmaPerWave; ++r) {
@@ -250,6 +293,10 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     // allocation tight): at j = 0 the PV half multiplies P = 0 with the V
     // stage zeroed below (adds exactly +0 to O); at j = wave_tiles the S half
     // reads a stage inside LDS and its result is never used.
+    // A split wavefront whose range starts after the workgroup's first tile
+    // runs the GEMM phases before it too: its P is still zero there (PV adds
+    // exactly +0; the V tile is finite cache data) and those S tiles are
+    // never softmaxed.  One skip condition keeps the accumulators in place.
     auto gemm_phase = [&](int j) {
         if (j > wave_tiles) return;
         constexpr int kRing = kPfAhead + 1;
@@ -285,18 +332,29 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     };
 
     // Softmax phase of tile j: mask, running max (lazy), P = 2^(c*s - m), row sum.
+    // Masked scores: -1e30 as the reference adds (src/kernels.rs:1242-1257).
+    // The split form may have rows with every key of a range masked (the
+    // range starts past the row's position); -inf gives them p = 0 and so
+    // O = 0, LSE = -1e30, weight 0 in the merge (the reference's -1e30 gives
+    // such rows p = 1 and an LSE near -1.3e29: also weight 0).
+    constexpr float kMasked = kSplit ? -__builtin_inff() : kPfNegBig;
     auto softmax_phase = [&](int j) {
-        if (j < 0 || j >= wave_tiles) return;
-        const int n0 = j * kPfBN;
-        const bool need_mask = (n0 + kPfBN - 1 > pos0) || (n0 + kPfBN > a.kv_len);
+        if (j < wave_t0 || j >= wave_tiles) return;
+        const int n0 = (tile0 + j) * kPfBN;
+        bool need_mask = (n0 + kPfBN - 1 > pos0) || (n0 + kPfBN > a.kv_len);
+        if constexpr (kSplit) need_mask = need_mask || n0 < key_lo || n0 + kPfBN > key_hi;
         if (need_mask) {
-            const int qpos = pos0 + l32;
+            // Keys n in [key_lo, n_end) stay, n_end = min(position + 1, key_hi,
+            // kv_len) clamped to >= key_lo: one unsigned compare per score.
+            const int n_end = max(key_lo, min(min(pos0 + l32 + 1, key_hi), a.kv_len));
+            const uint32_t span = static_cast<uint32_t>(n_end - key_lo);
+            const int rel0 = n0 - key_lo + 4 * hl;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int n = n0 + 32 * mb + 8 * (r >> 2) + 4 * hl + (r & 3);
-                    if (n > qpos || n >= a.kv_len) s[mb][r] = kPfNegBig;
+                    const int rel = rel0 + 32 * mb + 8 * (r >> 2) + (r & 3);
+                    if (static_cast<uint32_t>(rel) >= span) s[mb][r] = kMasked;
                 }
         }
         // P = 2^(c*s - m) with the running max m as it stands; the row sum
@@ -379,6 +437,29 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     const int row = row0 + l32;
     const float lt = l_run + swap_halves(l_run);
     const float l_safe = fmaxf(lt, 1.0e-8f);
+    if constexpr (kSplit) {
+        // Logical tile (q block, head group) = bq * (Hq/GROUP) + qh/GROUP; its
+        // row r = (row % BM) * GROUP + qh % GROUP in split-major scratch
+        // (src/kernels.rs:2105-2141).  Rows past q_len (zero Q) are written
+        // too, as the reference's padded tile rows are.
+        const int m_eff = a.block_m * a.split_group;
+        const int64_t tile = static_cast<int64_t>(row / a.block_m) * (a.num_q_heads / a.split_group) +
+                             qh / a.split_group;
+        const int64_t prow = (tile * a.num_splits + blockIdx.y) * m_eff +
+                             (row % a.block_m) * a.split_group + qh % a.split_group;
+        uint16_t* prow_p = a.att_partial + prow * kHeadDim;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                half4_t h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) h[e] = static_cast<half_t>(o[db][4 * i + e] / l_safe);
+                *reinterpret_cast<half4_t*>(prow_p + 32 * db + 8 * i + 4 * hl) = h;
+            }
+        if (hl == 0) a.lse_partial[prow] = m_run + log2f(l_safe);
+        return;
+    }
     if (row < a.q_len) {
         uint16_t* orow = a.out + (static_cast<int64_t>(row) * a.num_q_heads + qh) * kHeadDim;
 #pragma unroll
@@ -399,9 +480,71 @@ static int32_t launch_prefill(PrefillArgs a, int num_kv_heads, hipStream_t strea
     a.blocks_per_head = (a.tasks_per_head + kPfWaves - 1) / kPfWaves;
     const int64_t blocks = static_cast<int64_t>(a.blocks_per_head) * num_kv_heads;
     if (blocks > 0x7fffffff) return GROUT_ERR_KV_LEN;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3(static_cast<unsigned>(blocks)),
                        dim3(kPfWaves * kWave), 0, stream, a);
     return launch_status();
+}
+
+// Merge of the split-K partials (prefill_splitk_reduce_merge,
+// src/kernels.rs:2151-2323): thread = (row < q_len, q head, 8 dims); weights
+// w_s = 2^(lse_s - max) / max(sum, 1e-8), out = f16(sum_s w_s * att_s).
+__global__ __launch_bounds__(256) void attn_prefill_split_merge_kernel(
+    const uint16_t* __restrict__ att, const float* __restrict__ lse, uint16_t* __restrict__ out,
+    int num_q_heads, int q_len, int block_m, int group, int num_splits) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t total = static_cast<int64_t>(q_len) * num_q_heads * (kHeadDim / 8);
+    if (idx >= total) return;
+    const int d0 = static_cast<int>(idx % (kHeadDim / 8)) * 8;
+    const int64_t rh = idx / (kHeadDim / 8);
+    const int head = static_cast<int>(rh % num_q_heads);
+    const int row = static_cast<int>(rh / num_q_heads);
+    const int m_eff = block_m * group;
+    const int64_t tile = static_cast<int64_t>(row / block_m) * (num_q_heads / group) + head / group;
+    const int r = (row % block_m) * group + head % group;
+    const float* l = lse + tile * num_splits * m_eff + r;
+    float mx = l[0];
+    for (int s = 1; s < num_splits; ++s) mx = fmaxf(mx, l[static_cast<int64_t>(s) * m_eff]);
+    float sum = 0.0f;
+    for (int s = 0; s < num_splits; ++s) sum += __builtin_amdgcn_exp2f(l[static_cast<int64_t>(s) * m_eff] - mx);
+    const float inv = 1.0f / fmaxf(sum, 1.0e-8f);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint16_t* p = att + (tile * num_splits * m_eff + r) * kHeadDim + d0;
+    for (int s = 0; s < num_splits; ++s) {
+        const float w = __builtin_amdgcn_exp2f(l[static_cast<int64_t>(s) * m_eff] - mx) * inv;
+        const half8_t x = load_half8(p + static_cast<int64_t>(s) * m_eff * kHeadDim);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(x[e]) * w;
+    }
+    half8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = static_cast<half_t>(acc[e]);
+    store_half8(out + (static_cast<int64_t>(row) * num_q_heads + head) * kHeadDim + d0, o);
+}
+
+static int32_t launch_prefill_split(PrefillArgs a, int num_kv_heads, hipStream_t stream) {
+    const int64_t q_blocks = (static_cast<int64_t>(a.q_len) + a.block_m - 1) / a.block_m;
+    const int64_t pos_tiles = q_blocks * (a.block_m / kPfRows);
+    const int64_t tasks = pos_tiles * a.group;
+    const int64_t bph = (tasks + kPfWaves - 1) / kPfWaves;
+    const int64_t blocks = bph * num_kv_heads;
+    if (pos_tiles > 0x3fffffff || blocks > 0x7fffffff) return GROUT_ERR_KV_LEN;
+    a.n_pos_tiles = static_cast<int>(pos_tiles);
+    a.tasks_per_head = static_cast<int>(tasks);
+    a.blocks_per_head = static_cast<int>(bph);
+    hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3(static_cast<unsigned>(blocks), a.num_splits),
+                       dim3(kPfWaves * kWave), 0, stream, a);
+    return launch_status();
+}
+
+// Scratch geometry of the split-K form: tiles = ceil(q_len/BM) * (Hq/GROUP),
+// rows per tile num_splits * BM * GROUP (src/kernels.rs:1922-1944).
+static int64_t prefill_split_rows(int32_t num_q_heads, int32_t q_len, int32_t block_m,
+                                  int32_t group, int32_t num_splits) {
+    if (num_q_heads <= 0 || q_len < 0 || block_m <= 0 || group <= 0 || num_splits <= 0 ||
+        num_q_heads % group != 0)
+        return GROUT_ERR_ARG;
+    const int64_t tiles = (static_cast<int64_t>(q_len) + block_m - 1) / block_m * (num_q_heads / group);
+    return tiles * num_splits * block_m * group;
 }
 
 }  // namespace grout
@@ -442,4 +585,93 @@ extern "C" int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache
     a.query_start = query_start;
     a.max_seq_len = max_seq_len;
     return launch_prefill(a, num_kv_heads, to_hip(stream));
+}
+
+extern "C" int32_t grout_attn_prefill_split(const uint16_t* q, const uint16_t* k_cache,
+                                            const uint16_t* v_cache, uint16_t* att_partial,
+                                            float* lse_partial, float qk_scale, int32_t num_q_heads,
+                                            int32_t num_kv_heads, int32_t head_dim, int32_t q_len,
+                                            int32_t kv_len, int32_t query_start,
+                                            int32_t max_seq_len, int32_t block_m, int32_t block_n,
+                                            int32_t group, int32_t num_splits,
+                                            grout_stream_t stream) {
+    // The prefill checks, plus the microbench's group check
+    // (benchmarks/src/bin/attention_microbench.rs:411-421) and this
+    // kernel's tile limits.
+    GROUT_REQUIRE_PTR(q);
+    GROUT_REQUIRE_PTR(k_cache);
+    GROUT_REQUIRE_PTR(v_cache);
+    GROUT_REQUIRE_PTR(att_partial);
+    GROUT_REQUIRE_PTR(lse_partial);
+    GROUT_REQUIRE(head_dim == kHeadDim, GROUT_ERR_HEAD_DIM);
+    GROUT_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
+                  GROUT_ERR_HEADS);
+    GROUT_REQUIRE(max_seq_len > 0, GROUT_ERR_SEQ_RANGE);
+    GROUT_REQUIRE(q_len >= 0 && query_start >= 0, GROUT_ERR_KV_LEN);
+    GROUT_REQUIRE(kv_len >= 1 && kv_len <= max_seq_len, GROUT_ERR_KV_LEN);
+    GROUT_REQUIRE(qk_scale > 0.0f && qk_scale < 1.0e30f, GROUT_ERR_ARG);
+    GROUT_REQUIRE(group >= 1 && (num_q_heads / num_kv_heads) % group == 0, GROUT_ERR_GROUP);
+    GROUT_REQUIRE(block_m >= kPfRows && block_m % kPfRows == 0 && block_m <= 65536, GROUT_ERR_ARG);
+    GROUT_REQUIRE(block_n >= 1 && block_n <= 65536, GROUT_ERR_SPLITS);
+    GROUT_REQUIRE(num_splits >= 1 && num_splits <= GROUT_MAX_PREFILL_SPLITS, GROUT_ERR_SPLITS);
+    if (q_len == 0) return GROUT_OK;
+
+    PrefillArgs a = {};
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.out = nullptr;
+    a.scale_log2 = qk_scale / logf(2.0f);
+    a.num_q_heads = num_q_heads;
+    a.group = num_q_heads / num_kv_heads;
+    a.q_len = q_len;
+    a.kv_len = kv_len;
+    a.query_start = query_start;
+    a.max_seq_len = max_seq_len;
+    a.att_partial = att_partial;
+    a.lse_partial = lse_partial;
+    a.block_m = block_m;
+    a.block_n = block_n;
+    a.split_group = group;
+    a.num_splits = num_splits;
+    return launch_prefill_split(a, num_kv_heads, to_hip(stream));
+}
+
+extern "C" int32_t grout_attn_prefill_split_merge(const uint16_t* att_partial,
+                                                  const float* lse_partial, uint16_t* out,
+                                                  int32_t num_q_heads, int32_t head_dim,
+                                                  int32_t q_len, int32_t block_m, int32_t group,
+                                                  int32_t num_splits, grout_stream_t stream) {
+    GROUT_REQUIRE_PTR(att_partial);
+    GROUT_REQUIRE_PTR(lse_partial);
+    GROUT_REQUIRE_PTR(out);
+    GROUT_REQUIRE(head_dim == kHeadDim, GROUT_ERR_HEAD_DIM);
+    GROUT_REQUIRE(num_q_heads > 0, GROUT_ERR_HEADS);
+    GROUT_REQUIRE(q_len >= 0, GROUT_ERR_KV_LEN);
+    GROUT_REQUIRE(group >= 1 && num_q_heads % group == 0, GROUT_ERR_GROUP);
+    GROUT_REQUIRE(block_m >= 1 && block_m <= 65536, GROUT_ERR_ARG);
+    GROUT_REQUIRE(num_splits >= 1 && num_splits <= GROUT_MAX_PREFILL_SPLITS, GROUT_ERR_SPLITS);
+    if (q_len == 0) return GROUT_OK;
+    const int64_t threads = static_cast<int64_t>(q_len) * num_q_heads * (kHeadDim / 8);
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffff) return GROUT_ERR_KV_LEN;
+    hipLaunchKernelGGL(attn_prefill_split_merge_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       to_hip(stream), att_partial, lse_partial, out, num_q_heads, q_len, block_m,
+                       group, num_splits);
+    return launch_status();
+}
+
+extern "C" int64_t grout_attn_prefill_split_partial_bytes(int32_t num_q_heads, int32_t head_dim,
+                                                          int32_t q_len, int32_t block_m,
+                                                          int32_t group, int32_t num_splits) {
+    if (head_dim <= 0) return GROUT_ERR_ARG;
+    const int64_t rows = prefill_split_rows(num_q_heads, q_len, block_m, group, num_splits);
+    return rows < 0 ? rows : rows * head_dim * 2;
+}
+
+extern "C" int64_t grout_attn_prefill_split_lse_bytes(int32_t num_q_heads, int32_t q_len,
+                                                      int32_t block_m, int32_t group,
+                                                      int32_t num_splits) {
+    const int64_t rows = prefill_split_rows(num_q_heads, q_len, block_m, group, num_splits);
+    return rows < 0 ? rows : rows * 4;
 }

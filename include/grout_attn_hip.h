@@ -61,6 +61,7 @@ const char* grout_status_string(int32_t status);
 #define GROUT_HEAD_DIM 128
 #define GROUT_MAX_DECODE_GROUP 16
 #define GROUT_MAX_DECODE_SPLITS 1024
+#define GROUT_MAX_PREFILL_SPLITS 1024
 
 /* --------------------------------------------------------- RoPE table (A1) */
 /* Replaces build_inv_freq (src/model.rs:5992-6003): host-side, f32,
@@ -144,6 +145,47 @@ int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uin
                            int32_t num_kv_heads, int32_t head_dim, int32_t q_len,
                            int32_t kv_len, int32_t query_start, int32_t max_seq_len,
                            grout_stream_t stream);
+
+/* --------------------------------------------------- split-K prefill (A8) */
+/* Replaces fmha_prefill_gqa_lpt_split (src/kernels.rs:1872-2142), launched by
+ * the attention microbench (benchmarks/src/bin/attention_microbench.rs:418-469)
+ * with generics BM = block_m, BN = block_n, GROUP = group, NUM_KV_SPLITS =
+ * num_splits.  Same Q/cache layouts and masking as grout_attn_prefill (cache
+ * head stride max_seq_len).  Logical tile (q block b, head group hg) has index
+ * b * (num_q_heads/group) + hg and rows r = bm*group + g = query row
+ * b*block_m + bm of q head hg*group + g (zero Q past q_len).  Split s of q
+ * block b covers keys of the tiles [s*tps, min(s*tps+tps, tc)) of block_n
+ * keys, tc = ceil(min(query_start+(b+1)*block_m, kv_len)/block_n),
+ * tps = ceil(tc/num_splits).
+ *   att_partial [tiles, num_splits*block_m*group, 128] f16, row
+ *   s*block_m*group + r: f16(acc/max(l,1e-8)) over the split's keys;
+ *   lse_partial [tiles, num_splits*block_m*group] f32, m + log2(max(l,1e-8)).
+ * A row with no key in a split's range stores O = 0, LSE = -1e30 (weight 0 in
+ * the merge; the reference stores another weight-0 value there).
+ * block_m must be a multiple of 32; group must divide num_q_heads/num_kv_heads.
+ * Sizes: grout_attn_prefill_split_partial_bytes / _lse_bytes. */
+int32_t grout_attn_prefill_split(const uint16_t* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, uint16_t* att_partial,
+                                 float* lse_partial, float qk_scale, int32_t num_q_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t q_len,
+                                 int32_t kv_len, int32_t query_start, int32_t max_seq_len,
+                                 int32_t block_m, int32_t block_n, int32_t group,
+                                 int32_t num_splits, grout_stream_t stream);
+
+/* Replaces prefill_splitk_reduce_merge (src/kernels.rs:2151-2323): for rows
+ * below q_len, out[row, head, :] = f16(sum_s w_s * att_s) with
+ * w_s = 2^(lse_s - max) / max(sum, 1e-8); out [q_len, num_q_heads, 128]. */
+int32_t grout_attn_prefill_split_merge(const uint16_t* att_partial, const float* lse_partial,
+                                       uint16_t* out, int32_t num_q_heads, int32_t head_dim,
+                                       int32_t q_len, int32_t block_m, int32_t group,
+                                       int32_t num_splits, grout_stream_t stream);
+
+/* Scratch bytes of grout_attn_prefill_split (< 0: invalid arguments). */
+int64_t grout_attn_prefill_split_partial_bytes(int32_t num_q_heads, int32_t head_dim,
+                                               int32_t q_len, int32_t block_m, int32_t group,
+                                               int32_t num_splits);
+int64_t grout_attn_prefill_split_lse_bytes(int32_t num_q_heads, int32_t q_len, int32_t block_m,
+                                           int32_t group, int32_t num_splits);
 
 /* ------------------------------------------------ split-K GQA decode (A9) */
 /* Replaces fmha_decode_gqa_split (src/kernels.rs:2586-2749) as recorded at

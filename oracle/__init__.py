@@ -58,6 +58,9 @@ def lib():
         L.go_attn_decode_merge.argtypes = [_u16p, _f32p, _u16p] + [_i32] * 4
         L.go_decode_split_range.argtypes = [_i32] * 4 + [ctypes.POINTER(_i32)] * 2
         L.go_kv_cache_update_seq.argtypes = [_u16p] * 4 + [_i32] * 5
+        L.go_attn_prefill_split.argtypes = (
+            [_u16p] * 4 + [_f32p, ctypes.c_float] + [_i32] * 12)
+        L.go_attn_prefill_split_merge.argtypes = [_u16p, _f32p, _u16p] + [_i32] * 6
         _lib = L
     return _lib
 
@@ -171,3 +174,28 @@ def kv_cache_update_seq(new_k, new_v, k_cache, v_cache, position_start: int):
     S, Hkv, D = new_k.shape
     lib().go_kv_cache_update_seq(_u16(new_k), _u16(new_v), _u16(k_cache), _u16(v_cache),
                                  position_start, S, Hkv, D, k_cache.shape[1])
+
+
+def attn_prefill_split(q, k_cache, v_cache, qk_scale: float, kv_len: int, query_start: int,
+                       block_m: int, block_n: int, group: int, num_splits: int,
+                       nthreads: int = 0):
+    """q [S, Hq, D] -> (att_partial [tiles, NKS*BM*group, D] f16, lse [tiles, NKS*BM*group])."""
+    S, Hq, D = q.shape
+    Hkv, max_seq, _ = k_cache.shape
+    tiles = -(-S // block_m) * (Hq // group)
+    ns_m = num_splits * block_m * group
+    att = np.zeros((tiles, ns_m, D), dtype=np.float16)
+    lse = np.zeros((tiles, ns_m), dtype=np.float32)
+    lib().go_attn_prefill_split(
+        _u16(q), _u16(k_cache), _u16(v_cache), _u16(att), _f32(lse), float(qk_scale), Hq, Hkv,
+        D, S, kv_len, query_start, max_seq, block_m, block_n, group, num_splits, nthreads)
+    return att, lse
+
+
+def attn_prefill_split_merge(att, lse, num_q_heads: int, q_len: int, block_m: int, group: int,
+                             num_splits: int) -> np.ndarray:
+    D = att.shape[2]
+    out = np.zeros((q_len, num_q_heads, D), dtype=np.float16)
+    lib().go_attn_prefill_split_merge(_u16(att), _f32(lse), _u16(out), num_q_heads, D, q_len,
+                                      block_m, group, num_splits)
+    return out

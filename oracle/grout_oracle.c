@@ -442,3 +442,170 @@ void go_kv_cache_update_seq(const uint16_t* new_k, const uint16_t* new_v, uint16
         }
     }
 }
+
+/* src/kernels.rs:1872-2142 fmha_prefill_gqa_lpt_split (generics BM, BN, GROUP,
+ * NUM_KV_SPLITS; M_EFF = BM*GROUP), with the K/V head stride taken from the
+ * cache (max_seq_len), not kv_len (src/kernels.rs:1922-1928 assumes
+ * kv_len == max_seq_len).  Logical tile = (q block b, head group hg), index
+ * b*num_head_groups + hg (:1998); tile row r = bm*GROUP + g is query row
+ * b*BM + bm of q head hg*GROUP + g (:2017-2024), zero Q beyond q_len (the
+ * tensor view's out-of-bounds fill); KV head hg*GROUP / (Hq/Hkv) (:1999).
+ * Split s covers KV tiles [s*tps, min(s*tps+tps, tc)) with
+ * tc = ceil(min(m_end, kv_len)/BN), tps = ceil(tc/NKS) (:2036-2043); tiles
+ * at or past mask_start = min((query_start+b*BM)/BN, kv_len/BN) get the
+ * additive -1e30 mask for n >= kv_len or n > query position (:2063-2075);
+ * rows beyond kv_len read as zero.  Per tile: m_ij = max(m_i, rowmax(qk)*c),
+ * p = 2^(qk*c - m_ij), l = l*alpha + sum(p), acc = acc*alpha + f16(p) V
+ * (:2077-2102); c = qk_scale / ln 2.  Stores att = f16(acc / max(l, 1e-8))
+ * at [tile, s*M_EFF + r, :] and lse = m + log2(max(l, 1e-8)) at
+ * [tile, s*M_EFF + r] (:2105-2141). */
+void go_attn_prefill_split(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           uint16_t* att_partial, float* lse_partial, float qk_scale,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t q_len, int32_t kv_len, int32_t query_start,
+                           int32_t max_seq_len, int32_t block_m, int32_t block_n,
+                           int32_t group, int32_t num_splits, int32_t nthreads) {
+    const int32_t D = head_dim, BM = block_m, BN = block_n, GR = group, NKS = num_splits;
+    const int32_t qgs = num_q_heads / num_kv_heads;
+    const int32_t num_q_blocks = (q_len + BM - 1) / BM;
+    const int32_t num_head_groups = num_q_heads / GR;
+    const int32_t m_eff = BM * GR;
+    const float c = qk_scale / logf(2.0f);
+    const int64_t tasks = (int64_t)num_q_blocks * num_head_groups * NKS;
+#ifdef _OPENMP
+    int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel num_threads(nt)
+#endif
+    {
+        float* qf = (float*)malloc((size_t)m_eff * D * sizeof(float));
+        float* acc = (float*)malloc((size_t)m_eff * D * sizeof(float));
+        float* qk = (float*)malloc((size_t)m_eff * BN * sizeof(float));
+        float* kt = (float*)malloc((size_t)BN * D * sizeof(float));
+        float* vt = (float*)malloc((size_t)BN * D * sizeof(float));
+        uint16_t* ph = (uint16_t*)malloc((size_t)m_eff * BN * sizeof(uint16_t));
+        float* mi = (float*)malloc((size_t)m_eff * sizeof(float));
+        float* li = (float*)malloc((size_t)m_eff * sizeof(float));
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int64_t t = 0; t < tasks; ++t) {
+            const int32_t split = (int32_t)(t % NKS);
+            const int64_t tile = t / NKS;
+            const int32_t b = (int32_t)(tile / num_head_groups);
+            const int32_t hg = (int32_t)(tile % num_head_groups);
+            const int32_t kvh = hg * GR / qgs;
+            for (int32_t r = 0; r < m_eff; ++r) {
+                const int32_t row = b * BM + r / GR, head = hg * GR + r % GR;
+                for (int32_t d = 0; d < D; ++d) {
+                    qf[(int64_t)r * D + d] =
+                        row < q_len ? h2f(q[((int64_t)row * num_q_heads + head) * D + d]) : 0.0f;
+                    acc[(int64_t)r * D + d] = 0.0f;
+                }
+                mi[r] = 0.0f - 1.0e30f;
+                li[r] = 0.0f;
+            }
+            const int32_t m_end = query_start + (b + 1) * BM;
+            const int32_t k_seqlen_tiles = kv_len / BN;
+            int32_t mask_start = (query_start + b * BM) / BN;
+            if (mask_start > k_seqlen_tiles) mask_start = k_seqlen_tiles;
+            const int32_t lim = m_end < kv_len ? m_end : kv_len;
+            const int32_t tc = (lim + BN - 1) / BN;
+            const int32_t tps = (tc + NKS - 1) / NKS;
+            const int32_t st = split * tps;
+            const int32_t et = st + tps < tc ? st + tps : tc;
+            const uint16_t* kh = k_cache + (int64_t)kvh * max_seq_len * D;
+            const uint16_t* vh = v_cache + (int64_t)kvh * max_seq_len * D;
+            for (int32_t j = st; j < et; ++j) {
+                for (int32_t n = 0; n < BN; ++n) {
+                    const int32_t tok = j * BN + n;
+                    const int ok = tok < kv_len && tok < max_seq_len;
+                    for (int32_t d = 0; d < D; ++d) {
+                        kt[n * D + d] = ok ? h2f(kh[(int64_t)tok * D + d]) : 0.0f;
+                        vt[n * D + d] = ok ? h2f(vh[(int64_t)tok * D + d]) : 0.0f;
+                    }
+                }
+                for (int32_t r = 0; r < m_eff; ++r) {
+                    const int32_t mpos = query_start + b * BM + r / GR;
+                    float rmax = 0.0f - 1.0e30f;
+                    for (int32_t n = 0; n < BN; ++n) {
+                        float dot = 0.0f;
+                        for (int32_t d = 0; d < D; ++d) dot += qf[(int64_t)r * D + d] * kt[n * D + d];
+                        if (j >= mask_start) {
+                            const int32_t na = j * BN + n;
+                            const int keep = na < kv_len && mpos >= na;
+                            dot = dot + (keep ? 0.0f : 0.0f - 1.0e30f);
+                        }
+                        qk[(int64_t)r * BN + n] = dot;
+                        rmax = n == 0 ? dot : fmaxf(rmax, dot);
+                    }
+                    const float m_ij = fmaxf(mi[r], rmax * c);
+                    float l_ij = 0.0f;
+                    for (int32_t n = 0; n < BN; ++n) {
+                        const float p = exp2f(qk[(int64_t)r * BN + n] * c - m_ij);
+                        l_ij += p;
+                        ph[(int64_t)r * BN + n] = go_f32_to_f16(p);
+                    }
+                    const float alpha = exp2f(mi[r] - m_ij);
+                    li[r] = li[r] * alpha + l_ij;
+                    for (int32_t d = 0; d < D; ++d) {
+                        float a = acc[(int64_t)r * D + d] * alpha;
+                        float pv = 0.0f;
+                        for (int32_t n = 0; n < BN; ++n) pv += h2f(ph[(int64_t)r * BN + n]) * vt[n * D + d];
+                        acc[(int64_t)r * D + d] = a + pv;
+                    }
+                    mi[r] = m_ij;
+                }
+            }
+            const int64_t base = tile * (int64_t)NKS * m_eff + (int64_t)split * m_eff;
+            for (int32_t r = 0; r < m_eff; ++r) {
+                const float l_safe = fmaxf(li[r], 1.0e-8f);
+                for (int32_t d = 0; d < D; ++d)
+                    att_partial[(base + r) * D + d] = go_f32_to_f16(acc[(int64_t)r * D + d] / l_safe);
+                lse_partial[base + r] = mi[r] + log2f(l_safe);
+            }
+        }
+        free(qf); free(acc); free(qk); free(kt); free(vt); free(ph); free(mi); free(li);
+    }
+}
+
+/* src/kernels.rs:2151-2323 prefill_splitk_reduce_merge: per tile row r,
+ * w_s = 2^(lse_s - max_s lse) / max(sum, 1e-8) (:2273-2289) and
+ * out[row, head, :] = f16(sum_s w_s * f32(att_s)) (:2291-2320), written for
+ * rows below q_len only. */
+void go_attn_prefill_split_merge(const uint16_t* att_partial, const float* lse_partial,
+                                 uint16_t* out, int32_t num_q_heads, int32_t head_dim,
+                                 int32_t q_len, int32_t block_m, int32_t group,
+                                 int32_t num_splits) {
+    const int32_t D = head_dim, BM = block_m, GR = group, NKS = num_splits;
+    const int32_t num_q_blocks = (q_len + BM - 1) / BM;
+    const int32_t num_head_groups = num_q_heads / GR;
+    const int32_t m_eff = BM * GR;
+    float* w = (float*)malloc((size_t)NKS * sizeof(float));
+    for (int64_t tile = 0; tile < (int64_t)num_q_blocks * num_head_groups; ++tile) {
+        const int32_t b = (int32_t)(tile / num_head_groups);
+        const int32_t hg = (int32_t)(tile % num_head_groups);
+        for (int32_t r = 0; r < m_eff; ++r) {
+            const int32_t row = b * BM + r / GR, head = hg * GR + r % GR;
+            if (row >= q_len) continue;
+            const float* lse = lse_partial + tile * (int64_t)NKS * m_eff;
+            float mx = lse[r];
+            for (int32_t s = 1; s < NKS; ++s) mx = fmaxf(mx, lse[(int64_t)s * m_eff + r]);
+            float sum = 0.0f;
+            for (int32_t s = 0; s < NKS; ++s) {
+                w[s] = exp2f(lse[(int64_t)s * m_eff + r] - mx);
+                sum += w[s];
+            }
+            const float safe = fmaxf(sum, 1.0e-8f);
+            for (int32_t s = 0; s < NKS; ++s) w[s] = w[s] / safe;
+            for (int32_t d = 0; d < D; ++d) {
+                float a = 0.0f;
+                for (int32_t s = 0; s < NKS; ++s) {
+                    const int64_t prow = tile * (int64_t)NKS * m_eff + (int64_t)s * m_eff + r;
+                    a += h2f(att_partial[prow * D + d]) * w[s];
+                }
+                out[((int64_t)row * num_q_heads + head) * D + d] = go_f32_to_f16(a);
+            }
+        }
+    }
+    free(w);
+}

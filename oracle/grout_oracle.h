@@ -85,6 +85,22 @@ void go_kv_cache_update_seq(const uint16_t* new_k, const uint16_t* new_v, uint16
                             uint16_t* v_cache, int32_t position_start, int32_t seq_len,
                             int32_t num_kv_heads, int32_t head_dim, int32_t max_seq);
 
+/* src/kernels.rs:1872-2142 fmha_prefill_gqa_lpt_split (cache head stride
+ * max_seq_len): att_partial [tiles, NKS*BM*GROUP, D] f16, lse_partial
+ * [tiles, NKS*BM*GROUP] f32, tiles = ceil(q_len/BM) * (Hq/GROUP). */
+void go_attn_prefill_split(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           uint16_t* att_partial, float* lse_partial, float qk_scale,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t q_len, int32_t kv_len, int32_t query_start,
+                           int32_t max_seq_len, int32_t block_m, int32_t block_n,
+                           int32_t group, int32_t num_splits, int32_t nthreads);
+
+/* src/kernels.rs:2151-2323 prefill_splitk_reduce_merge -> out [q_len, Hq, D]. */
+void go_attn_prefill_split_merge(const uint16_t* att_partial, const float* lse_partial,
+                                 uint16_t* out, int32_t num_q_heads, int32_t head_dim,
+                                 int32_t q_len, int32_t block_m, int32_t group,
+                                 int32_t num_splits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -110,6 +110,43 @@ def test_prefill_checks(L):
     assert call(ql=0) == 0
 
 
+def test_prefill_split_checks(L):
+    f = L.grout_attn_prefill_split
+    ok = dict(q=A, k=A, v=A, att=A, lse=A, sc=0.088, hq=8, hkv=2, D=128, ql=40, kv=40, qs=0,
+              MS=64, bm=32, bn=32, gr=2, ns=3)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return f(a["q"], a["k"], a["v"], a["att"], a["lse"], a["sc"], a["hq"], a["hkv"], a["D"],
+                 a["ql"], a["kv"], a["qs"], a["MS"], a["bm"], a["bn"], a["gr"], a["ns"], S)
+
+    assert call(lse=0) == -1
+    assert call(att=U) == -2
+    assert call(D=64) == -3
+    assert call(hq=7) == -4
+    assert call(kv=65) == -6
+    assert call(gr=3) == -7            # group must divide q_group_size (4)
+    assert call(gr=0) == -7
+    assert call(bm=48) == -9           # block_m a multiple of 32
+    assert call(bm=16) == -9
+    assert call(bn=0) == -8
+    assert call(ns=0) == -8
+    assert call(ns=1025) == -8
+    assert call(ql=0) == 0
+    mg = L.grout_attn_prefill_split_merge
+    # att, lse, out, Hq, D, q_len, BM, group, NKS
+    assert mg(A, A, 0, 8, 128, 40, 32, 2, 3, S) == -1
+    assert mg(A, A, A, 8, 64, 40, 32, 2, 3, S) == -3
+    assert mg(A, A, A, 8, 128, 40, 32, 3, 3, S) == -7
+    assert mg(A, A, A, 8, 128, 40, 32, 2, 0, S) == -8
+    assert mg(A, A, A, 8, 128, 0, 32, 2, 3, S) == 0
+    # Scratch: ceil(40/32) * (8/2) tiles of 3 * 32 * 2 rows.
+    rows = 2 * 4 * 3 * 32 * 2
+    assert L.grout_attn_prefill_split_partial_bytes(8, 128, 40, 32, 2, 3) == rows * 128 * 2
+    assert L.grout_attn_prefill_split_lse_bytes(8, 40, 32, 2, 3) == rows * 4
+    assert L.grout_attn_prefill_split_lse_bytes(8, 40, 32, 3, 3) < 0
+
+
 def test_decode_split_merge_checks(L):
     sp = L.grout_attn_decode_split
     # q, k, v, att, lse, scale, pos, hkv, G, D, MS, BN, NKS

@@ -344,3 +344,116 @@ def test_kv_cache_update_seq_leaves_other_slots():
     assert np.array_equal(v[:, start:start + S], nv.transpose(1, 0, 2))
     assert (k[:, :start] == 7).all() and (k[:, start + S:] == 7).all()
     assert (v[:, :start] == -3).all() and (v[:, start + S:] == -3).all()
+
+
+# ------------------------------------------------------- split-K prefill --
+
+def _split_range_tiles(b, bm, bn, ns, s, kv_len, qs):
+    """Split s of q block b: KV tiles [s*tps, min(s*tps+tps, tc)) with
+    tc = ceil(min(qs+(b+1)*bm, kv_len)/bn), tps = ceil(tc/ns)
+    (src/kernels.rs:2036-2043), computed here from the formula's text."""
+    tc = -(-min(qs + (b + 1) * bm, kv_len) // bn)
+    tps = -(-tc // ns)
+    return s * tps, min(s * tps + tps, tc)
+
+
+def _prefill_split_f64(q, kc, vc, scale, kv_len, qs, bm, bn, gr, ns):
+    """Independent float64 statement of every partial: the softmax of each
+    (row, head) over the causal keys of its split's range, its LSE in log2
+    units, and the reference layout [tile, s*BM*GR + bm*GR + g]."""
+    S, hq, _ = q.shape
+    hkv = kc.shape[0]
+    nb = -(-S // bm)
+    ngrp = hq // gr
+    att = np.zeros((nb * ngrp, ns * bm * gr, D))
+    lse = np.full((nb * ngrp, ns * bm * gr), np.nan)
+    for b in range(nb):
+        for s in range(ns):
+            t0, t1 = _split_range_tiles(b, bm, bn, ns, s, kv_len, qs)
+            lo, hi = t0 * bn, min(t1 * bn, kv_len)
+            for i in range(bm):
+                row = b * bm + i
+                pos = qs + row
+                for h in range(hq):
+                    tile, r = b * ngrp + h // gr, s * bm * gr + i * gr + h % gr
+                    kv = h // (hq // hkv)
+                    keys = np.arange(lo, min(hi, pos + 1))
+                    if len(keys) == 0:
+                        lse[tile, r] = -np.inf  # empty or fully masked: zero weight
+                        continue
+                    qv = q[row, h].astype(np.float64) if row < S else np.zeros(D)
+                    z = kc[kv, keys].astype(np.float64) @ qv * scale
+                    w = np.exp(z - z.max())
+                    att[tile, r] = w / w.sum() @ vc[kv, keys].astype(np.float64)
+                    lse[tile, r] = (z.max() + np.log(w.sum())) / math.log(2)
+    return att, lse
+
+
+@pytest.mark.parametrize("S,qs,kv_len,hq,hkv,bm,bn,gr,ns", [
+    (40, 0, 40, 4, 2, 32, 32, 2, 3),     # ragged q_len, GROUP = q group size
+    (64, 0, 64, 4, 2, 32, 16, 1, 4),     # GROUP 1, BN not the kernel tile
+    (33, 7, 40, 6, 3, 64, 32, 2, 2),     # query_start > 0, padded rows
+    (48, 0, 48, 8, 2, 16, 8, 4, 5),      # small tiles, many splits
+])
+def test_prefill_split_partials_match_float64(S, qs, kv_len, hq, hkv, bm, bn, gr, ns):
+    g = rng(30)
+    MS = kv_len + 3
+    q, kc, vc = normal_f16(g, (S, hq, D)), normal_f16(g, (hkv, MS, D)), normal_f16(g, (hkv, MS, D))
+    att, lse = oracle.attn_prefill_split(q, kc, vc, SCALE, kv_len, qs, bm, bn, gr, ns)
+    att64, lse64 = _prefill_split_f64(q, kc, vc, SCALE, kv_len, qs, bm, bn, gr, ns)
+    live = np.isfinite(lse64)
+    assert live.any()
+    assert np.max(np.abs(att.astype(np.float64)[live] - att64[live])) < 2e-3
+    assert np.max(np.abs(lse[live] - lse64[live])) < 1e-4
+    # Empty ranges store O = 0, LSE = -1e30 exactly; ranges whose keys are all
+    # masked for a row (the split starts past its position) carry a finite
+    # partial but an LSE below -1e28, i.e. weight 0 in the merge.
+    assert np.all(lse[~live] < -1e28)
+    out = oracle.attn_prefill_split_merge(att, lse, hq, S, bm, gr, ns).astype(np.float32)
+    ref = _attn_f64(q, kc, vc, SCALE, kv_len, qs)
+    assert np.max(np.abs(out - ref)) < 2e-3
+
+
+def test_prefill_split_empty_splits_and_invariance():
+    g = rng(31)
+    S, hq, hkv = 20, 4, 2
+    q, kc, vc = normal_f16(g, (S, hq, D)), normal_f16(g, (hkv, S, D)), normal_f16(g, (hkv, S, D))
+    # One 32-row block over 20 keys: tc = 1 tile of 32, so splits 1.. are empty.
+    att, lse = oracle.attn_prefill_split(q, kc, vc, SCALE, S, 0, 32, 32, 2, 4)
+    ns_m = 32 * 2
+    assert np.all(att[:, ns_m:] == 0) and np.all(lse[:, ns_m:] == np.float32(-1e30))
+    outs = []
+    for ns in (1, 2, 7):
+        a, l = oracle.attn_prefill_split(q, kc, vc, SCALE, S, 0, 32, 4, 2, ns)
+        outs.append(oracle.attn_prefill_split_merge(a, l, hq, S, 32, 2, ns).astype(np.float32))
+    full = oracle.attn_prefill_f32(q, kc, vc, SCALE, S, 0)
+    for o in outs:
+        assert np.max(np.abs(o - full)) < 2e-3
+    # Row 0 of every head sees key 0 only: exactly V[0] through the merge.
+    for h in range(hq):
+        assert np.array_equal(outs[2][0, h], vc[h // 2, 0].astype(np.float32))
+
+
+def test_prefill_split_merge_closed_forms():
+    bm, gr, ns, hq, S = 16, 1, 2, 1, 16
+    att = np.zeros((1, ns * bm * gr, D), dtype=np.float16)
+    att[0, :bm] = 1.0      # split 0
+    att[0, bm:] = 4.0      # split 1
+    lse = np.zeros((1, ns * bm * gr), dtype=np.float32)
+    out = oracle.attn_prefill_split_merge(att, lse, hq, S, bm, gr, ns)
+    assert np.all(out == np.float16(2.5))  # equal LSE -> mean
+    lse[0, bm:] = 1.0  # split 1 twice as heavy (log2 units)
+    out = oracle.attn_prefill_split_merge(att, lse, hq, S, bm, gr, ns)
+    assert np.allclose(out.astype(np.float32), (1.0 + 2 * 4.0) / 3, atol=2e-3)
+    # Layout: row r = bm*GROUP + g of tile b*ngroups + hg is (row b*BM+bm, head hg*GROUP+g).
+    bm, gr, hq, S = 2, 2, 4, 3
+    att = np.zeros((2 * 2, bm * gr, D), dtype=np.float16)
+    for tile in range(4):
+        for r in range(bm * gr):
+            att[tile, r] = tile * 10 + r
+    lse = np.zeros((4, bm * gr), dtype=np.float32)
+    out = oracle.attn_prefill_split_merge(att, lse, hq, S, bm, gr, 1)
+    for row in range(S):
+        for h in range(hq):
+            b, i, hg, gg = row // bm, row % bm, h // gr, h % gr
+            assert out[row, h, 0] == (b * 2 + hg) * 10 + i * gr + gg
