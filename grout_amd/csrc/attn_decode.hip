@@ -224,6 +224,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     __shared__ __attribute__((aligned(16))) half_t q_lds[GROUT_MAX_DECODE_GROUP * kHeadDim];
     __shared__ float s_cos[64], s_sin[64];
     __shared__ uint32_t s_flag;
+    __shared__ uint32_t s_next_sub;  // next sub-chunk of the split not yet taken by a wavefront
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -281,13 +282,19 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     const int tok_begin = tb * a.block_n;
     const int tok_end = (tb < te) ? min(te * a.block_n, s_kv) : tok_begin;
     const int nsub = (tok_end - tok_begin + kDecSubTok - 1) / kDecSubTok;
-    const int nk = nsub > wave ? (nsub - wave + kDecWaves - 1) / kDecWaves : 0;  // this wave's sub-chunks
+    // The first kDecWaveStages sub-chunks of each wavefront are fixed
+    // (w, w+4, w+8, w+12); after that a wavefront takes the next untaken
+    // sub-chunk from an LDS counter whenever a stage of its ring frees, so
+    // the four wavefronts finish within about one sub-chunk of each other.
+    const int nk = nsub > wave ? (nsub - wave + kDecWaves - 1) / kDecWaves : 0;
+    const int n_first = min(kDecWaveStages, nk);
+    if (tid == 0) s_next_sub = kDecWaves * kDecWaveStages;
 
     const uint16_t* kh = a.k_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
     const uint16_t* vh = a.v_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
 
-    // Sub-chunk copy: this wavefront's k-th sub-chunk (tokens t0 + [0,16),
-    // t0 = tok_begin + 16*(wave + 4k)) lands in its stage k%4.  Copy i moves
+    // Sub-chunk copy: sub-chunk `sub` of the split (tokens t0 + [0,16),
+    // t0 = tok_begin + 16*sub), this wavefront's k-th, lands in its stage k%4.  Copy i moves
     // token rows 4i..4i+3: 1 KB contiguous in the cache, 1 KB contiguous in
     // LDS.  Lane l takes row tr = 4i + l/16 and source chunk (l%16) ^ swz(tr),
     // so LDS chunk c of row tr holds global chunk c ^ swz(tr): the MFMA operand
@@ -296,8 +303,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     const uint32_t lds0 = static_cast<uint32_t>(
         (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(lds)));
     const uint32_t wave_lds = lds0 + static_cast<uint32_t>(wave) * kDecWaveBytes;
-    auto issue_sub = [&](int k) {
-        const int t0 = tok_begin + kDecSubTok * (wave + kDecWaves * k);
+    auto issue_sub = [&](int k, int sub) {
+        const int t0 = tok_begin + kDecSubTok * sub;
         const uint32_t kb = wave_lds + (k % kDecWaveStages) * 2 * kDecSubBytes;
         const uint32_t vb = kb + kDecSubBytes;
         const uint16_t* kbase = kh + static_cast<int64_t>(t0) * kHeadDim;
@@ -314,10 +321,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
 
 #pragma unroll
     for (int k = 0; k < kDecWaveStages; ++k)
-        if (k < nk) issue_sub(k);
+        if (k < n_first) issue_sub(k, wave + kDecWaves * k);
     // Wave 0's prologue copies are older than its sub-chunk copies (8 each).
     if (wave == 0) {
-        const int later = min(kDecWaveStages, nk);
+        const int later = n_first;
         if (later >= 4) {
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(32));
         } else if (later == 3) {
@@ -397,11 +404,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             qop[c] = (n < G) ? *reinterpret_cast<const half8_t*>(qsrc + n * kHeadDim + 32 * c + 8 * qgrp)
                              : half8_t{};
     }
-    // Sub-chunk (wavefront, index) and row of the new position (owner only).
+    // Sub-chunk and row of the new position (owner split only).
     const int pos_local = static_cast<int>(pos) - tok_begin;
     const int sub_pos = owns_new_row ? pos_local / kDecSubTok : -1;
-    const bool wave_owns = owns_new_row && (sub_pos % kDecWaves) == wave;
-    const int k_pos = wave_owns ? sub_pos / kDecWaves : -1;
     const int tr_pos = pos_local % kDecSubTok;
 
     float m = kNegBig;
@@ -425,10 +430,15 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             v_off[db] = kDecSubBytes + tr * 256 + 16 * ((2 * db + ((n & 3) >> 1)) ^ dec_swz(tr)) + 8 * (n & 1);
     }
 
-    for (int k = 0; k < nk; ++k) {
+    // Sub-chunks in this wavefront's stages k%4 .. (k+3)%4: q0 (the current
+    // one) .. q3; n_issued counts the sub-chunks it has issued so far.
+    int q0 = wave, q1 = wave + kDecWaves, q2 = wave + 2 * kDecWaves, q3 = wave + 3 * kDecWaves;
+    int n_issued = n_first;
+    bool more = n_first == kDecWaveStages;  // untaken sub-chunks may remain
+    for (int k = 0; k < n_issued; ++k) {
         // Sub-chunk k has landed once only the copies of this wavefront's later
         // sub-chunks (8 each, up to three) are outstanding.
-        const int younger = min(kDecWaveStages - 1, nk - 1 - k);
+        const int younger = min(kDecWaveStages - 1, n_issued - 1 - k);
         if (younger >= 3) {
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(24));
         } else if (younger == 2) {
@@ -439,7 +449,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
         }
         unsigned char* kb = lds + wave * kDecWaveBytes + (k % kDecWaveStages) * 2 * kDecSubBytes;
-        if (k == k_pos) {
+        if (q0 == sub_pos) {
             // The copy read the cache before the new row was stored: lanes
             // 0-15 put the rotated K row, lanes 16-31 the V row into row
             // tr_pos (swizzled).  A wavefront's LDS accesses complete in order.
@@ -460,12 +470,27 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         for (int cc = 0; cc < 4; ++cc) ka[cc] = *reinterpret_cast<const half8_t*>(kb + k_off[cc]);
 #pragma unroll
         for (int db = 0; db < 8; ++db) va[db] = lds_read_tr16(reinterpret_cast<const half_t*>(kb + v_off[db]));
-        if (k + kDecWaveStages < nk) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue_sub(k + kDecWaveStages);
+        const int cur = q0;
+        int next = -1;
+        if (more) {
+            uint32_t got = 0;
+            if (lane == 0) got = __hip_atomic_fetch_add(&s_next_sub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            next = __builtin_amdgcn_readfirstlane(static_cast<int>(got));
+            if (next < nsub) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue_sub(k + kDecWaveStages, next);
+                ++n_issued;
+            } else {
+                next = -1;
+                more = false;
+            }
         }
+        q0 = q1;
+        q1 = q2;
+        q2 = q3;
+        q3 = next;
 
-        const int t = tok_begin + kDecSubTok * (wave + kDecWaves * k);  // first token
+        const int t = tok_begin + kDecSubTok * cur;  // first token
         // S^T[token, head]: lane holds head n, tokens t + 4qgrp + r.
         float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
