@@ -128,6 +128,26 @@ def bench_prefill(torch, ga, steps, warmup, gen):
                 hq=hq, hkv=hkv, S=S)
 
 
+def bench_prefill_split(torch, ga, pre, steps, num_splits=4, block_m=128, block_n=64):
+    """Split-K prefill (fmha_prefill_gqa_lpt_split + merge) on the c3 inputs of
+    bench_prefill: per-launch event times of the split kernel and of the merge."""
+    q, kc, vc = pre["q"], pre["kc"], pre["vc"]
+    S, hq, hkv = pre["S"], pre["hq"], pre["hkv"]
+    gr = hq // hkv
+    att, lse = ga.prefill_split_scratch(hq, S, block_m, gr, num_splits)
+    out = torch.empty_like(q)
+    fn = lambda: ga.attend_prefill_split(q, kc, vc, att, lse, 0, block_m, block_n, gr,  # noqa
+                                         num_splits)
+    durs, _ = time_launches(torch, fn, steps, 5)
+    mfn = lambda: ga.prefill_splitk_reduce_merge(att, lse, out, block_m, gr, num_splits)  # noqa
+    mdurs, _ = time_launches(torch, mfn, steps, 5)
+    diff = (out.float() - pre["out"].float()).abs().max().item()
+    ms, mms = sum(durs) / len(durs), sum(mdurs) / len(mdurs)
+    return dict(ms=ms, merge_ms=mms, tflops=pre["flops"] / ((ms + mms) * 1e-3) / 1e12,
+                max_diff_vs_unsplit=diff, num_splits=num_splits, block_m=block_m,
+                block_n=block_n, group=gr)
+
+
 def bench_norm(torch, ga, steps, warmup, gen):
     hq, hkv, S = 32, 8, 8192
     q = torch.randn((S, hq, D), device="cuda", generator=gen).half()
@@ -315,7 +335,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "norm", "kv", "mfma-probe"],
+    ap.add_argument("--only", choices=["all", "prefill", "prefill-split", "decode", "norm", "kv",
+                                       "mfma-probe"],
                     default="all",
                     help="run one workload only (for profiling runs); prints no JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -361,6 +382,12 @@ def main(argv=None) -> int:
         elif args.only == "kv":
             kvu = bench_kv_update(torch, ga, args.steps, args.warmup, gen)
             log(f"kv update c3: {kvu['ms'] * 1e3:.1f} us, {kvu['gbs']:.0f} GB/s")
+        elif args.only == "prefill-split":
+            pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
+            psp = bench_prefill_split(torch, ga, pre, args.steps)
+            log(f"prefill c3: {pre['ms'] * 1e3:.1f} us; split-K: split {psp['ms'] * 1e3:.1f} us + "
+                f"merge {psp['merge_ms'] * 1e3:.1f} us, max |split - unsplit| "
+                f"{psp['max_diff_vs_unsplit']:.2e}")
         elif args.only == "mfma-probe":
             mp = bench_mfma_probe(torch)
             log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
@@ -375,6 +402,10 @@ def main(argv=None) -> int:
     log("prefill c3 ...")
     pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
     log(f"prefill c3: {pre['ms']:.3f} ms/launch, {pre['tflops']:.1f} TFLOP/s")
+    log("prefill split-K c3 ...")
+    psp = bench_prefill_split(torch, ga, pre, args.steps)
+    log(f"prefill split-K c3: split {psp['ms'] * 1e3:.1f} us + merge {psp['merge_ms'] * 1e3:.1f} us, "
+        f"{psp['tflops']:.1f} TFLOP/s, max |split - unsplit| {psp['max_diff_vs_unsplit']:.2e}")
     log("mfma probe ...")
     mp = bench_mfma_probe(torch)
     log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
@@ -450,6 +481,11 @@ def main(argv=None) -> int:
             "hip_graph_packet_capture": GRAPH_PACKET_CAPTURE,
             "cpu_baseline": cpu_dec,
         },
+        "prefill_split_c3": {
+            "split_us": round(psp["ms"] * 1e3, 2), "merge_us": round(psp["merge_ms"] * 1e3, 2),
+            "TFLOP/s": round(psp["tflops"], 1), "num_splits": psp["num_splits"],
+            "block_m": psp["block_m"], "block_n": psp["block_n"], "group": psp["group"],
+            "max_abs_diff_vs_unsplit": psp["max_diff_vs_unsplit"]},
         "decode_c2": {"us_per_step": round(dec2["step_us"], 3),
                       "fused_kernel_us": round(dec2["fused_us"], 3),
                       "fused_gbs": round(dec2["fused_gbs"], 1),
