@@ -252,6 +252,61 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
         kc=kc, vc=vc, q=q_out[:hq].clone())
 
 
+def gemv_bytes(m: int, k: int) -> int:
+    """Weight [m, k] and x [k] read once, out [m] written (f16)."""
+    return 2 * (m * k + k + m)
+
+
+def bench_decode_layer(torch, ga, steps, gen):
+    """The decode-layer ops of the c4 model (Qwen3-32B: hidden 5120, 64 Q / 8 KV
+    heads, vocab 151936) through the C entry points, back to back.  Each GEMV
+    cycles through enough weight copies (>= 600 MB) that no launch finds its
+    weight in the 256 MB last-level cache, as in a real token step where 64
+    layers' weights pass between two reads of one matrix."""
+    L = ga.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for name, m, k in (("qkv_proj", 10240, 5120), ("o_proj", 5120, 8192),
+                       ("lm_head", 151936, 5120)):
+        copies = max(1, -(-600_000_000 // (2 * m * k)))
+        ws = [(torch.randn((m, k), device="cuda", generator=gen) * (k ** -0.5)).half()
+              for _ in range(copies)]
+        x = torch.randn((k,), device="cuda", generator=gen).half()
+        out = torch.empty((m,), device="cuda", dtype=torch.float16)
+        ga.gemv_f16(ws[0], x, out)  # argument checks of the Python mirror once
+        ptrs = [w.data_ptr() for w in ws]
+        it = [0]
+
+        def fn():
+            it[0] += 1
+            return L.grout_gemv_f16(ptrs[it[0] % copies], x.data_ptr(), out.data_ptr(), m, k, st)
+
+        n = max(steps, 60) if m * k < 1 << 28 else max(steps, 20)
+        ms = time_back_to_back(torch, fn, n, 2 * copies)
+        nb = gemv_bytes(m, k)
+        res[name] = dict(m=m, k=k, us=ms * 1e3, gbs=nb / (ms * 1e-3) / 1e9, bytes=nb,
+                         weight_copies=copies)
+        del ws
+    n = 5120
+    r = torch.randn((n,), device="cuda", generator=gen).half()
+    x = torch.randn((n,), device="cuda", generator=gen).half()
+    w = (1 + 0.1 * torch.randn((n,), device="cuda", generator=gen)).half()
+    o = torch.empty_like(r)
+    ro = torch.empty_like(r)
+    args = (r.data_ptr(), x.data_ptr(), w.data_ptr(), o.data_ptr(), ro.data_ptr(), EPS, n, st)
+    res["add_rms_norm"] = dict(n=n, us=1e3 * time_back_to_back(
+        torch, lambda: L.grout_add_rms_norm_decode(*args), max(steps, 200), 20))
+    v = 151936
+    lg = torch.randn((v,), device="cuda", generator=gen).half()
+    bm, bi = ga.argmax_scratch(v)
+    tok = torch.empty((1,), device="cuda", dtype=torch.int32)
+    aargs = (lg.data_ptr(), bm.data_ptr(), bi.data_ptr(), tok.data_ptr(), v, st)
+    res["argmax"] = dict(n=v, us=1e3 * time_back_to_back(
+        torch, lambda: L.grout_argmax_f16(*aargs), max(steps, 200), 20))
+    assert int(tok.item()) == int(torch.argmax(lg.float()).item()), "argmax mismatch"
+    return res
+
+
 def bench_mfma_probe(torch, launches: int = 8):
     """Sustained v_mfma_f32_32x32x16_f16 rate for operands distributed like the
     prefill kernel's (grout_amd/probe/mfma_ceiling.hip): mode 0 = both N(0,1)
@@ -336,7 +391,7 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "prefill", "prefill-split", "decode", "norm", "kv",
-                                       "mfma-probe"],
+                                       "mfma-probe", "decode-layer"],
                     default="all",
                     help="run one workload only (for profiling runs); prints no JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -388,6 +443,11 @@ def main(argv=None) -> int:
             log(f"prefill c3: {pre['ms'] * 1e3:.1f} us; split-K: split {psp['ms'] * 1e3:.1f} us + "
                 f"merge {psp['merge_ms'] * 1e3:.1f} us, max |split - unsplit| "
                 f"{psp['max_diff_vs_unsplit']:.2e}")
+        elif args.only == "decode-layer":
+            dl = bench_decode_layer(torch, ga, args.steps, gen)
+            log("decode layer c4: " + ", ".join(
+                f"{k} {v['us']:.2f} us" + (f" ({v['gbs']:.0f} GB/s)" if "gbs" in v else "")
+                for k, v in dl.items()))
         elif args.only == "mfma-probe":
             mp = bench_mfma_probe(torch)
             log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
@@ -421,6 +481,11 @@ def main(argv=None) -> int:
         f"fused kernel {dec['fused_us']:.2f} us ({dec['fused_gbs']:.0f} GB/s), "
         f"split {dec['split_us']:.2f} us ({dec['split_gbs']:.0f} GB/s), "
         f"merge {dec['merge_us']:.2f} us, NKS={dec['num_splits']}")
+    log("decode layer ops c4 ...")
+    dl = bench_decode_layer(torch, ga, args.steps, gen)
+    log("decode layer c4: " + ", ".join(
+        f"{k} {v['us']:.2f} us" + (f" ({v['gbs']:.0f} GB/s)" if "gbs" in v else "")
+        for k, v in dl.items()))
     log("decode c2 ...")
     dec2 = bench_decode(torch, ga, 32, 8, 4096, 200, 20, gen, 200)
     log(f"decode c2: graph step {dec2['step_us']:.2f} us, fused {dec2['fused_us']:.2f} us, "
@@ -490,6 +555,13 @@ def main(argv=None) -> int:
                       "fused_kernel_us": round(dec2["fused_us"], 3),
                       "fused_gbs": round(dec2["fused_gbs"], 1),
                       "num_splits": dec2["num_splits"]},
+        "decode_layer_c4": {
+            **{nm: {"m": dl[nm]["m"], "k": dl[nm]["k"], "us": round(dl[nm]["us"], 2),
+                    "GB/s": round(dl[nm]["gbs"], 1),
+                    "frac_of_hbm_peak": round(dl[nm]["gbs"] / PEAK_HBM_GBS, 4)}
+               for nm in ("qkv_proj", "o_proj", "lm_head")},
+            "add_rms_norm_us": round(dl["add_rms_norm"]["us"], 2),
+            "argmax_us": round(dl["argmax"]["us"], 2)},
         "qk_norm_rope_c3": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                             "frac_of_hbm_peak": round(nrm["gbs"] / PEAK_HBM_GBS, 4)},
         "kv_cache_update_c3": {"us": round(kvu["ms"] * 1e3, 2), "GB/s": round(kvu["gbs"], 1),

@@ -39,7 +39,8 @@ __all__ = [
     "GroutError", "LibraryMissing", "lib", "build_inv_freq", "qk_norm_rope_kv_prefill",
     "qk_norm_rope_kv_decode", "attend_prefill", "fmha_decode_gqa_split",
     "splitk_reduce_merge", "decode_fused", "attend_prefill_split", "prefill_split_scratch",
-    "prefill_splitk_reduce_merge", "decode_scratch", "decode_counters",
+    "prefill_splitk_reduce_merge", "add_rms_norm_decode", "gemv_f16", "argmax_scratch",
+    "argmax_f16", "decode_scratch", "decode_counters",
     "pick_num_splits", "DecodeGraphRunner",
     "HEAD_DIM", "ATTN_BN_DECODE",
 ]
@@ -275,6 +276,52 @@ def prefill_splitk_reduce_merge(att_partial, lse_partial, out, block_m: int, gro
         _ptr(att_partial), _ptr(lse_partial), _ptr(out), Hq, D, q_len, block_m, group,
         num_splits, _stream()), "prefill_splitk_reduce_merge")
     return out
+
+
+def add_rms_norm_decode(residual, x, weight, out, residual_out, eps: float):
+    """add_rms_norm_decode_raw_f16 (src/kernels.rs:3076-3216) on one hidden row:
+    residual_out = residual + x, out = RMSNorm(residual_out) * weight."""
+    n = residual.numel()
+    args = ((residual, "residual"), (x, "x"), (weight, "weight"), (out, "out"),
+            (residual_out, "residual_out"))
+    for t, nm in args:
+        _ensure(t.numel() == n, f"{nm} must have {n} elements, got {t.numel()}")
+    for t, nm in args:
+        _f16(t, nm)
+    _check(lib().grout_add_rms_norm_decode(_ptr(residual), _ptr(x), _ptr(weight), _ptr(out),
+                                           _ptr(residual_out), float(eps), n, _stream()),
+           "add_rms_norm_decode")
+    return out, residual_out
+
+
+def gemv_f16(weight, x, out):
+    """cuBLAS GemvInPlace (src/cublas.rs:572-607): out[m] = weight[m, k] @ x[k], f32 accumulate."""
+    _ensure(weight.dim() == 2, f"weight must be [m, k], got {list(weight.shape)}")
+    m, k = weight.shape
+    _ensure(x.numel() == k, f"x must have {k} elements, got {x.numel()}")
+    _ensure(out.numel() == m, f"out must have {m} elements, got {out.numel()}")
+    for t, nm in ((weight, "weight"), (x, "x"), (out, "out")):
+        _f16(t, nm)
+    _check(lib().grout_gemv_f16(_ptr(weight), _ptr(x), _ptr(out), m, k, _stream()), "gemv_f16")
+    return out
+
+
+def argmax_scratch(n: int, device="cuda"):
+    """Per-block scratch of :func:`argmax_f16` for n logits."""
+    torch = _torch()
+    nb = int(lib().grout_argmax_blocks(n))
+    _ensure(nb > 0, "argmax needs at least one logit")
+    return (torch.empty((nb,), dtype=torch.float32, device=device),
+            torch.empty((nb,), dtype=torch.int32, device=device))
+
+
+def argmax_f16(logits, block_max, block_idx, token):
+    """argmax_blocks_f16 + argmax_reduce_blocks_to_u32 (src/kernels.rs:345-505):
+    token[0] = lowest index of the largest logit."""
+    _f16(logits, "logits")
+    _check(lib().grout_argmax_f16(_ptr(logits), _ptr(block_max), _ptr(block_idx), _ptr(token),
+                                  logits.numel(), _stream()), "argmax_f16")
+    return token
 
 
 def pick_num_splits(max_context: int, num_kv_heads: int, block_n: int = ATTN_BN_DECODE,

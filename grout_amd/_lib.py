@@ -60,6 +60,10 @@ SIGNATURES = {
     "grout_attn_prefill_split_merge": (c_i32, [c_vp] * 3 + [c_i32] * 6 + [c_vp]),
     "grout_attn_prefill_split_partial_bytes": (c_i64, [c_i32] * 6),
     "grout_attn_prefill_split_lse_bytes": (c_i64, [c_i32] * 5),
+    "grout_add_rms_norm_decode": (c_i32, [c_vp] * 5 + [c_f32, c_i32, c_vp]),
+    "grout_gemv_f16": (c_i32, [c_vp] * 3 + [c_i32] * 2 + [c_vp]),
+    "grout_argmax_blocks": (c_i32, [c_i32]),
+    "grout_argmax_f16": (c_i32, [c_vp] * 4 + [c_i32, c_vp]),
     "grout_attn_decode_split": (
         c_i32, [c_vp] * 5 + [c_u16, c_vp] + [c_i32] * 6 + [c_vp]),
     "grout_attn_decode_merge": (c_i32, [c_vp] * 3 + [c_i32] * 4 + [c_vp]),

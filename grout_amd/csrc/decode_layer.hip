@@ -1,0 +1,323 @@
+// Decode-layer ops either side of the attention step: the fused residual add +
+// RMSNorm of one hidden row, the f16 GEMV of the QKV / output projections,
+// and the two-stage greedy argmax that turns logits into the next token.
+//
+// Replaces add_rms_norm_decode_raw_f16 (src/kernels.rs:3076-3216), the cuBLAS
+// GemvInPlace nodes of the decode graph (src/cublas.rs:572-607, recorded at
+// src/model.rs:3166-3175 and :3505-3512) and argmax_blocks_f16 +
+// argmax_reduce_blocks_to_u32 (src/kernels.rs:345-392, :458-505).
+//
+// All three are HBM- or latency-bound; the kernels are shaped for that:
+//  * the norm is one workgroup of 1024 threads holding the row in registers
+//    between the sum of squares and the normalisation (one read of each
+//    input, one write of each output);
+//  * the GEMV streams each weight row with all 256 threads of a workgroup
+//    (16-byte loads, up to 8 rows x 2 chunks in flight per thread) and
+//    accumulates in f32 with v_dot2_f32_f16 (exact f16 products);
+//  * the argmax reduces (value, index) pairs, the lowest index winning ties,
+//    in 2048-element blocks and then over the blocks.
+#include <math.h>
+
+#include "abi_util.h"
+#include "common.h"
+
+namespace grout {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------------ norm --
+
+constexpr int kNormThreads = 1024;
+constexpr int kNormChunks = 4;  // 16-byte chunks per thread: n <= 8 * 1024 * 4
+constexpr int kNormMaxN = 8 * kNormThreads * kNormChunks;
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_decode_kernel(
+    const uint16_t* residual, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ out, uint16_t* residual_out, float eps, int n) {
+    // residual_out may be residual itself (the decode graph updates the
+    // residual stream in place): each thread reads its chunks before the
+    // barrier and writes the same chunks after it.
+    __shared__ float red[kNormThreads / kWave];
+    const int tid = threadIdx.x;
+    float c[kNormChunks][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormChunks; ++k) {
+        const int i = (tid + k * kNormThreads) * 8;
+        if (i < n) {
+            const half8_t r8 = load_half8(residual + i);
+            const half8_t x8 = load_half8(x + i);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                c[k][e] = static_cast<float>(r8[e]) + static_cast<float>(x8[e]);
+                ss += c[k][e] * c[k][e];
+            }
+        }
+    }
+    ss = wave_sum_f32(ss);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / kWave; ++i) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int k = 0; k < kNormChunks; ++k) {
+        const int i = (tid + k * kNormThreads) * 8;
+        if (i < n) {
+#pragma clang fp contract(off)
+            const half8_t w8 = load_half8(w + i);
+            half8_t o, rs;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                o[e] = static_cast<half_t>((c[k][e] * inv) * static_cast<float>(w8[e]));
+                rs[e] = static_cast<half_t>(c[k][e]);
+            }
+            store_half8(out + i, o);
+            store_half8(residual_out + i, rs);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ GEMV --
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvUnroll = 2;  // 16-byte chunks per thread per row in flight
+constexpr int kGemvMaxK = 32768;
+
+__device__ __forceinline__ float dot8(half8_t a, half8_t b, float acc) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const half2_t a2 = {a[2 * p], a[2 * p + 1]};
+        const half2_t b2 = {b[2 * p], b[2 * p + 1]};
+        acc = __builtin_amdgcn_fdot2(a2, b2, acc, false);
+    }
+    return acc;
+}
+
+// Sums each of v[0..R) over the 64 lanes by recursive halving: at the step of
+// offset 32 the lanes with bit 5 set keep rows [R/2, R) and the others rows
+// [0, R/2), each adding its partner's half; after log2(R) such steps every
+// lane holds one row, and the remaining xor steps complete the sum.  Row r
+// ends in v[0] of lane r * (64 / R) (and the lanes above it up to the next
+// row).  6 + R - 1 shuffles instead of 6 R.
+template <int R>
+__device__ __forceinline__ float wave_multi_sum(float (&v)[R], int lane) {
+    int off = 32;
+#pragma unroll
+    for (int half = R / 2; half >= 1; half /= 2, off /= 2) {
+        const bool up = (lane & off) != 0;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float keep = up ? v[i + half] : v[i];
+            const float send = up ? v[i] : v[i + half];
+            v[i] = keep + __shfl_xor(send, off);
+        }
+    }
+#pragma unroll
+    for (; off > 0; off >>= 1) v[0] += __shfl_xor(v[0], off);
+    return v[0];
+}
+
+// Workgroup b computes out rows b*R + [0, R).  Thread t of the workgroup
+// reads the 16-byte chunks t, t + 256, ... of each of the R rows (4 KB of a
+// row per workgroup load step, contiguous), so a row of k halves is streamed
+// by all 256 threads at once and R * kGemvUnroll chunks per thread are in
+// flight.  x chunks come from global memory (the same chunk for all R rows;
+// every workgroup hits it in L2).  Products are exact in f32
+// (v_dot2_f32_f16); the sum order is per thread, then across lanes, then
+// across the four wavefronts.
+template <int R>
+__global__ __launch_bounds__(kGemvThreads) void gemv_f16_kernel(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, uint16_t* __restrict__ out,
+    int m, int k) {
+    __shared__ float red[kGemvThreads / kWave][R];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int nchunk = k / 8;
+    const int row0 = static_cast<int>(blockIdx.x) * R;
+    const half8_t* xc = reinterpret_cast<const half8_t*>(x);
+    const half8_t* wr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, m - 1);  // rows past m repeat the last (not stored)
+        wr[r] = reinterpret_cast<const half8_t*>(W + static_cast<int64_t>(row) * k);
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    int c = tid;
+    for (; c + kGemvThreads * (kGemvUnroll - 1) < nchunk; c += kGemvThreads * kGemvUnroll) {
+        half8_t wv[kGemvUnroll][R];
+        half8_t xv[kGemvUnroll];
+#pragma unroll
+        for (int u = 0; u < kGemvUnroll; ++u) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) wv[u][r] = wr[r][c + kGemvThreads * u];
+            xv[u] = xc[c + kGemvThreads * u];
+        }
+        // Keep every load of the step ahead of the first dot product: left to
+        // itself the scheduler interleaves them and waits for each in turn.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < kGemvUnroll; ++u)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = dot8(wv[u][r], xv[u], acc[r]);
+    }
+    if (c < nchunk) {
+        const half8_t xv = xc[c];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = dot8(wr[r][c], xv, acc[r]);
+    }
+    const float v = wave_multi_sum<R>(acc, lane);
+    constexpr int kStride = kWave / R;
+    if (lane % kStride == 0) red[wave][lane / kStride] = v;
+    __syncthreads();
+    if (tid < R && row0 + tid < m) {
+        float t = red[0][tid];
+#pragma unroll
+        for (int w = 1; w < kGemvThreads / kWave; ++w) t += red[w][tid];
+        out[row0 + tid] = __builtin_bit_cast(uint16_t, static_cast<half_t>(t));
+    }
+}
+
+// ---------------------------------------------------------------- argmax --
+
+constexpr int kArgmaxThreads = 256;
+constexpr int kArgmaxBlock = kArgmaxThreads * 8;  // logits per first-stage block
+
+// (v, i) beats (bv, bi) when larger, or equal with a lower index.
+__device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__device__ __forceinline__ void argmax_block_reduce(float& bv, int& bi, float* sv, int* si) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        argmax_take(bv, bi, ov, oi);
+    }
+    const int tid = threadIdx.x;
+    if ((tid & (kWave - 1)) == 0) {
+        sv[tid / kWave] = bv;
+        si[tid / kWave] = bi;
+    }
+    __syncthreads();
+    bv = sv[0];
+    bi = si[0];
+#pragma unroll
+    for (int wv = 1; wv < kArgmaxThreads / kWave; ++wv) argmax_take(bv, bi, sv[wv], si[wv]);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_blocks_kernel(
+    const uint16_t* __restrict__ logits, int n, float* __restrict__ block_max,
+    uint32_t* __restrict__ block_idx) {
+    __shared__ float sv[kArgmaxThreads / kWave];
+    __shared__ int si[kArgmaxThreads / kWave];
+    const int base = static_cast<int>(blockIdx.x) * kArgmaxBlock + threadIdx.x * 8;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (base + 8 <= n) {
+        const half8_t v = load_half8(logits + base);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) argmax_take(bv, bi, static_cast<float>(v[e]), base + e);
+    } else {
+        for (int e = 0; base + e < n; ++e)
+            argmax_take(bv, bi, static_cast<float>(__builtin_bit_cast(half_t, logits[base + e])), base + e);
+    }
+    argmax_block_reduce(bv, bi, sv, si);
+    if (threadIdx.x == 0) {
+        block_max[blockIdx.x] = bv;
+        block_idx[blockIdx.x] = static_cast<uint32_t>(bi);
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_reduce_kernel(
+    const float* __restrict__ block_max, const uint32_t* __restrict__ block_idx, int nblocks,
+    uint32_t* __restrict__ token) {
+    __shared__ float sv[kArgmaxThreads / kWave];
+    __shared__ int si[kArgmaxThreads / kWave];
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int b = threadIdx.x; b < nblocks; b += kArgmaxThreads)
+        argmax_take(bv, bi, block_max[b], static_cast<int>(block_idx[b]));
+    argmax_block_reduce(bv, bi, sv, si);
+    if (threadIdx.x == 0) token[0] = static_cast<uint32_t>(bi == 0x7fffffff ? 0 : bi);
+}
+
+}  // namespace grout
+
+using namespace grout;
+
+extern "C" int32_t grout_add_rms_norm_decode(const uint16_t* residual, const uint16_t* x,
+                                             const uint16_t* weight, uint16_t* out,
+                                             uint16_t* residual_out, float eps, int32_t n,
+                                             grout_stream_t stream) {
+    GROUT_REQUIRE_PTR(residual);
+    GROUT_REQUIRE_PTR(x);
+    GROUT_REQUIRE_PTR(weight);
+    GROUT_REQUIRE_PTR(out);
+    GROUT_REQUIRE_PTR(residual_out);
+    GROUT_REQUIRE(n >= 8 && n % 8 == 0 && n <= kNormMaxN, GROUT_ERR_ARG);
+    GROUT_REQUIRE(eps >= 0.0f && eps < 1.0e30f, GROUT_ERR_ARG);
+    hipLaunchKernelGGL(add_rms_norm_decode_kernel, dim3(1), dim3(kNormThreads), 0, to_hip(stream),
+                       residual, x, weight, out, residual_out, eps, n);
+    return launch_status();
+}
+
+extern "C" int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uint16_t* out,
+                                  int32_t m, int32_t k, grout_stream_t stream) {
+    GROUT_REQUIRE_PTR(weight);
+    GROUT_REQUIRE_PTR(x);
+    GROUT_REQUIRE(out != nullptr, GROUT_ERR_NULL_POINTER);
+    GROUT_REQUIRE((reinterpret_cast<uintptr_t>(out) & 1u) == 0, GROUT_ERR_ALIGNMENT);
+    GROUT_REQUIRE(m >= 1 && k >= 8 && k % 8 == 0 && k <= kGemvMaxK, GROUT_ERR_ARG);
+    // Rows per workgroup: 8 while that still gives >= 4 workgroups per CU
+    // (256 CUs), fewer for short outputs so the grid keeps every CU busy.
+    const int rows = m >= 8 * 1024 ? 8 : m >= 4 * 1024 ? 4 : m >= 2 * 1024 ? 2 : 1;
+    const unsigned blocks = static_cast<unsigned>((m + rows - 1) / rows);
+    const hipStream_t s = to_hip(stream);
+    const dim3 block(kGemvThreads);
+    switch (rows) {
+        case 8: hipLaunchKernelGGL(gemv_f16_kernel<8>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
+        case 4: hipLaunchKernelGGL(gemv_f16_kernel<4>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
+        case 2: hipLaunchKernelGGL(gemv_f16_kernel<2>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
+        default: hipLaunchKernelGGL(gemv_f16_kernel<1>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
+    }
+    return launch_status();
+}
+
+extern "C" int32_t grout_argmax_blocks(int32_t n) {
+    if (n < 1) return GROUT_ERR_ARG;
+    return (n + kArgmaxBlock - 1) / kArgmaxBlock;
+}
+
+extern "C" int32_t grout_argmax_f16(const uint16_t* logits, float* block_max, uint32_t* block_idx,
+                                    uint32_t* token, int32_t n, grout_stream_t stream) {
+    GROUT_REQUIRE_PTR(logits);
+    GROUT_REQUIRE(block_max != nullptr && block_idx != nullptr && token != nullptr,
+                  GROUT_ERR_NULL_POINTER);
+    GROUT_REQUIRE(((reinterpret_cast<uintptr_t>(block_max) | reinterpret_cast<uintptr_t>(block_idx) |
+                    reinterpret_cast<uintptr_t>(token)) & 3u) == 0,
+                  GROUT_ERR_ALIGNMENT);
+    GROUT_REQUIRE(n >= 1, GROUT_ERR_ARG);
+    const int nblocks = (n + kArgmaxBlock - 1) / kArgmaxBlock;
+    hipLaunchKernelGGL(argmax_blocks_kernel, dim3(nblocks), dim3(kArgmaxThreads), 0, to_hip(stream),
+                       logits, n, block_max, block_idx);
+    const int32_t st = launch_status();
+    if (st != GROUT_OK) return st;
+    hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(kArgmaxThreads), 0, to_hip(stream),
+                       block_max, block_idx, nblocks, token);
+    return launch_status();
+}

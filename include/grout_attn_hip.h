@@ -187,6 +187,32 @@ int64_t grout_attn_prefill_split_partial_bytes(int32_t num_q_heads, int32_t head
 int64_t grout_attn_prefill_split_lse_bytes(int32_t num_q_heads, int32_t q_len, int32_t block_m,
                                            int32_t group, int32_t num_splits);
 
+/* ------------------------------------- decode-layer ops around attention (N1) */
+/* Replaces add_rms_norm_decode_raw_f16 (src/kernels.rs:3076-3216) as recorded
+ * in the decode graph (src/model.rs:3151-3163, 3513-3526): for one row of n,
+ * combined = f32(residual) + f32(x); inv = 1/sqrt(sum(combined^2)/n + eps);
+ * out = f16(combined*inv*weight); residual_out = f16(combined).
+ * n a multiple of 8, at most 32768; buffers 16-byte aligned, out and
+ * residual_out may not alias the inputs. */
+int32_t grout_add_rms_norm_decode(const uint16_t* residual, const uint16_t* x,
+                                  const uint16_t* weight, uint16_t* out, uint16_t* residual_out,
+                                  float eps, int32_t n, grout_stream_t stream);
+
+/* Replaces the cuBLAS GemvInPlace nodes of the decode graph (src/cublas.rs:572-607:
+ * cublasGemmEx(OP_T, OP_N, m, 1, k) on a row-major [m, k] f16 weight):
+ * out[i] = f16(sum_j weight[i][j] * x[j]) with f32 accumulation.
+ * k a multiple of 8, at most 32768; weight and x 16-byte aligned. */
+int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uint16_t* out, int32_t m,
+                       int32_t k, grout_stream_t stream);
+
+/* Replaces argmax_blocks_f16 + argmax_reduce_blocks_to_u32 (src/kernels.rs:345-392,
+ * 458-505), the in-graph greedy token pick: *token = the lowest index of the
+ * largest f32(logits[i]) over [0, n) (NaN logits are never picked).
+ * block_max / block_idx: grout_argmax_blocks(n) entries of scratch each. */
+int32_t grout_argmax_blocks(int32_t n);
+int32_t grout_argmax_f16(const uint16_t* logits, float* block_max, uint32_t* block_idx,
+                         uint32_t* token, int32_t n, grout_stream_t stream);
+
 /* ------------------------------------------------ split-K GQA decode (A9) */
 /* Replaces fmha_decode_gqa_split (src/kernels.rs:2586-2749) as recorded at
  * src/model.rs:3428-3452.

@@ -61,6 +61,10 @@ def lib():
         L.go_attn_prefill_split.argtypes = (
             [_u16p] * 4 + [_f32p, ctypes.c_float] + [_i32] * 12)
         L.go_attn_prefill_split_merge.argtypes = [_u16p, _f32p, _u16p] + [_i32] * 6
+        L.go_add_rms_norm.argtypes = [_u16p] * 5 + [ctypes.c_float, _i32]
+        L.go_gemv_f16.argtypes = [_u16p] * 3 + [_i32] * 3
+        L.go_argmax_f16.restype = ctypes.c_uint32
+        L.go_argmax_f16.argtypes = [_u16p, _i32]
         _lib = L
     return _lib
 
@@ -199,3 +203,24 @@ def attn_prefill_split_merge(att, lse, num_q_heads: int, q_len: int, block_m: in
     lib().go_attn_prefill_split_merge(_u16(att), _f32(lse), _u16(out), num_q_heads, D, q_len,
                                       block_m, group, num_splits)
     return out
+
+
+def add_rms_norm(residual, x, w, eps: float):
+    """-> (out, residual_out), f16 [n] each."""
+    n = residual.shape[0]
+    out = np.zeros(n, dtype=np.float16)
+    res = np.zeros(n, dtype=np.float16)
+    lib().go_add_rms_norm(_u16(residual), _u16(x), _u16(w), _u16(out), _u16(res), float(eps), n)
+    return out, res
+
+
+def gemv_f16(w, x, nthreads: int = 0) -> np.ndarray:
+    """w [m, k] f16 row-major, x [k] f16 -> f16 [m]."""
+    m, k = w.shape
+    out = np.zeros(m, dtype=np.float16)
+    lib().go_gemv_f16(_u16(w), _u16(x), _u16(out), m, k, nthreads)
+    return out
+
+
+def argmax_f16(logits) -> int:
+    return int(lib().go_argmax_f16(_u16(logits), logits.shape[0]))

@@ -609,3 +609,61 @@ void go_attn_prefill_split_merge(const uint16_t* att_partial, const float* lse_p
     }
     free(w);
 }
+
+/* ------------------------------------------------- decode-layer ops (N1) -- */
+
+/* src/kernels.rs:3076-3216 add_rms_norm_decode_raw_f16 (one row of n):
+ * combined = f32(residual) + f32(x) (:3143-3146), ss = sum combined^2 (f32,
+ * sequential here; the reference's order is a per-lane sum then a tree),
+ * inv = 1 / sqrt(ss/n + eps) (:3149-3153), out = f16(combined*inv*w),
+ * residual_out = f16(combined) (:3183-3188). */
+void go_add_rms_norm(const uint16_t* residual, const uint16_t* x, const uint16_t* w,
+                     uint16_t* out, uint16_t* residual_out, float eps, int32_t n) {
+    float ss = 0.0f;
+    for (int32_t i = 0; i < n; ++i) {
+        float c = h2f(residual[i]) + h2f(x[i]);
+        ss += c * c;
+    }
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int32_t i = 0; i < n; ++i) {
+        float c = h2f(residual[i]) + h2f(x[i]);
+        out[i] = go_f32_to_f16((c * inv) * h2f(w[i]));
+        residual_out[i] = go_f32_to_f16(c);
+    }
+}
+
+/* src/cublas.rs:260-345, 572-607 GemvInPlace: cublasGemmEx(OP_T, OP_N, m, 1,
+ * k) over a row-major [m, k] f16 matrix: out[i] = f16(sum_j W[i][j] x[j]),
+ * f32 accumulation (CUBLAS_COMPUTE_32F_FAST_16F, the default at :74). */
+void go_gemv_f16(const uint16_t* w, const uint16_t* x, uint16_t* out, int32_t m, int32_t k,
+                 int32_t nthreads) {
+#ifdef _OPENMP
+    int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for num_threads(nt) schedule(static)
+#endif
+    for (int32_t i = 0; i < m; ++i) {
+        const uint16_t* row = w + (int64_t)i * k;
+        float acc = 0.0f;
+        for (int32_t j = 0; j < k; ++j) acc += h2f(row[j]) * h2f(x[j]);
+        out[i] = go_f32_to_f16(acc);
+    }
+    (void)nthreads;
+}
+
+/* src/kernels.rs:345-392 argmax_blocks_f16 + :458-505
+ * argmax_reduce_blocks_to_u32: the largest f32(logit) over [0, n), the lowest
+ * index among equal maxima (reduce_max, then reduce_min over the indices
+ * equal to it).  NaN logits are never chosen; 0 if every logit is NaN. */
+uint32_t go_argmax_f16(const uint16_t* logits, int32_t n) {
+    int64_t best = -1;
+    float bv = 0.0f;
+    for (int32_t i = 0; i < n; ++i) {
+        float v = h2f(logits[i]);
+        if (v != v) continue;
+        if (best < 0 || v > bv) {
+            bv = v;
+            best = i;
+        }
+    }
+    return best < 0 ? 0u : (uint32_t)best;
+}

@@ -101,6 +101,17 @@ void go_attn_prefill_split_merge(const uint16_t* att_partial, const float* lse_p
                                  int32_t q_len, int32_t block_m, int32_t group,
                                  int32_t num_splits);
 
+/* src/kernels.rs:3076-3216 add_rms_norm_decode_raw_f16 (one row of n). */
+void go_add_rms_norm(const uint16_t* residual, const uint16_t* x, const uint16_t* w,
+                     uint16_t* out, uint16_t* residual_out, float eps, int32_t n);
+
+/* src/cublas.rs:572-607 GemvInPlace: out[m] = f16(W[m,k] x[k]), f32 accumulation. */
+void go_gemv_f16(const uint16_t* w, const uint16_t* x, uint16_t* out, int32_t m, int32_t k,
+                 int32_t nthreads);
+
+/* src/kernels.rs:345-505 two-stage greedy argmax: lowest index of the largest logit. */
+uint32_t go_argmax_f16(const uint16_t* logits, int32_t n);
+
 #ifdef __cplusplus
 }
 #endif

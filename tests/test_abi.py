@@ -196,6 +196,35 @@ def test_kv_cache_update_checks(L):
     assert g(A, A, A, A, A + 2, 1, 2, 128, 16, S) == -2
 
 
+def test_decode_layer_checks(L):
+    f = L.grout_add_rms_norm_decode
+    # residual, x, weight, out, residual_out, eps, n, stream
+    assert f(A, 0, A, A, A, 1e-6, 5120, S) == -1
+    assert f(A, A, A, U, A, 1e-6, 5120, S) == -2
+    assert f(A, A, A, A, A, 1e-6, 0, S) == -9
+    assert f(A, A, A, A, A, 1e-6, 5124, S) == -9          # not a multiple of 8
+    assert f(A, A, A, A, A, 1e-6, 32776, S) == -9         # above the one-workgroup maximum
+    assert f(A, A, A, A, A, -1.0, 5120, S) == -9
+    g = L.grout_gemv_f16
+    # weight, x, out, m, k, stream
+    assert g(0, A, A, 8, 8, S) == -1
+    assert g(A, A, 0, 8, 8, S) == -1
+    assert g(U, A, A, 8, 8, S) == -2
+    assert g(A, A, A + 1, 8, 8, S) == -2                  # out needs 2-byte alignment only
+    assert g(A, A, A, 0, 8, S) == -9
+    assert g(A, A, A, 8, 12, S) == -9
+    assert g(A, A, A, 8, 32776, S) == -9
+    assert L.grout_argmax_blocks(0) == -9
+    assert [L.grout_argmax_blocks(n) for n in (1, 2048, 2049, 151936)] == [1, 1, 2, 75]
+    a = L.grout_argmax_f16
+    # logits, block_max, block_idx, token, n, stream
+    assert a(0, A, A, A, 10, S) == -1
+    assert a(A, A, 0, A, 10, S) == -1
+    assert a(U, A, A, A, 10, S) == -2
+    assert a(A, A + 2, A, A, 10, S) == -2
+    assert a(A, A, A, A, 0, S) == -9
+
+
 def test_graph_handle_checks(L):
     assert L.grout_graph_begin(None) == -10
     assert L.grout_graph_launch(None, None) == -10
@@ -259,3 +288,11 @@ def test_python_mirror_shape_errors():
         grout_amd.attend_prefill(q, cache, cache, torch.zeros((4, 4, 128), dtype=h), 0)
     with pytest.raises(grout_amd.GroutError, match="rank 3"):
         grout_amd.attend_prefill(q[0], cache, cache, q[0], 0)
+    wm = torch.zeros((16, 64), dtype=h)
+    with pytest.raises(grout_amd.GroutError, match="x must have 64 elements"):
+        grout_amd.gemv_f16(wm, torch.zeros(32, dtype=h), torch.zeros(16, dtype=h))
+    with pytest.raises(grout_amd.GroutError, match="out must have 16 elements"):
+        grout_amd.gemv_f16(wm, torch.zeros(64, dtype=h), torch.zeros(15, dtype=h))
+    with pytest.raises(grout_amd.GroutError, match="weight must have 64 elements"):
+        z = torch.zeros(64, dtype=h)
+        grout_amd.add_rms_norm_decode(z, z, torch.zeros(32, dtype=h), z, z, 1e-6)

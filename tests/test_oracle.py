@@ -457,3 +457,105 @@ def test_prefill_split_merge_closed_forms():
         for h in range(hq):
             b, i, hg, gg = row // bm, row % bm, h // gr, h % gr
             assert out[row, h, 0] == (b * 2 + hg) * 10 + i * gr + gg
+
+
+# ------------------------------------------------------ decode-layer ops --
+# add_rms_norm_decode_raw_f16 (src/kernels.rs:3076-3216), the cuBLAS GemvInPlace
+# of the decode graph (src/cublas.rs:572-607) and the two-stage greedy argmax
+# (src/kernels.rs:345-505).
+
+def _f16_ulp(v):
+    """Spacing of the f16 grid at |v| (normal range; 2^-24 below it)."""
+    a = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+@pytest.mark.parametrize("n,eps,seed", [(5120, 1e-6, 1), (4096, 1e-6, 2), (40, 0.5, 3),
+                                        (8, 1e-6, 4), (32768, 1e-6, 5)])
+def test_add_rms_norm_against_float64(n, eps, seed):
+    g = rng(900 + seed)
+    r, x = normal_f16(g, n, 2.0), normal_f16(g, n, 0.5)
+    w = (1.0 + 0.1 * g.standard_normal(n)).astype(np.float16)
+    out, res = oracle.add_rms_norm(r, x, w, eps)
+    c = r.astype(np.float64) + x.astype(np.float64)
+    assert np.all(f16_ulp_diff(res, c.astype(np.float16)) <= 1)
+    assert np.mean(res == c.astype(np.float16)) > 0.999
+    inv = 1.0 / np.sqrt(np.mean(c * c) + eps)
+    exp = c * inv * w.astype(np.float64)
+    # The f32 sum of n positive squares is within n * 2^-24 relative, so inv is
+    # within (n/2 + 2) * 2^-24; two more f32 roundings and the f16 rounding.
+    rel = (n / 2 + 6) * 2.0 ** -24
+    assert np.all(np.abs(out.astype(np.float64) - exp) <= _f16_ulp(exp) * 0.5 + rel * np.abs(exp))
+    assert np.mean(out == exp.astype(np.float16)) > 0.99
+
+
+def test_add_rms_norm_closed_forms():
+    n = 1024
+    h = np.float16
+    # residual + x = 1 everywhere, w = 1, eps = 3: inv = 1/sqrt(1 + 3) = 0.5.  A
+    # mean over n-1, eps outside the sqrt or a dropped residual all move it.
+    out, res = oracle.add_rms_norm(np.full(n, 0.75, h), np.full(n, 0.25, h), np.ones(n, h), 3.0)
+    assert np.all(res == h(1.0)) and np.all(out == h(0.5))
+    # The weight multiplies elementwise, the residual output is the raw sum.
+    w = np.arange(n, dtype=np.float64).astype(h) / h(64)
+    out, res = oracle.add_rms_norm(np.full(n, -3.0, h), np.full(n, 1.0, h), w, 0.0)
+    assert np.all(res == h(-2.0)) and np.array_equal(out, (-w.astype(np.float64)).astype(h))
+    # eps = 0: the output is invariant under power-of-two scaling of the inputs.
+    g = rng(910)
+    r, x, wn = normal_f16(g, n), normal_f16(g, n), normal_f16(g, n)
+    o1, r1 = oracle.add_rms_norm(r, x, wn, 0.0)
+    o2, r2 = oracle.add_rms_norm(r * h(8), x * h(8), wn, 0.0)
+    assert np.array_equal(o1, o2) and np.array_equal(r2, r1 * h(8))
+
+
+@pytest.mark.parametrize("m,k,seed", [(300, 512, 1), (64, 5120, 2), (17, 8, 3), (5, 8192, 4)])
+def test_gemv_against_float64(m, k, seed):
+    g = rng(920 + seed)
+    w = normal_f16(g, (m, k), 1.0 / math.sqrt(k))
+    x = normal_f16(g, k)
+    out = oracle.gemv_f16(w, x)
+    w64, x64 = w.astype(np.float64), x.astype(np.float64)
+    exp = w64 @ x64
+    # f32 accumulation of exact f16 products: |err| <= k * 2^-24 * sum|w x|,
+    # plus half an f16 ulp for the final rounding.
+    bound = _f16_ulp(exp) * 0.5 + k * 2.0 ** -24 * (np.abs(w64) @ np.abs(x64))
+    assert np.all(np.abs(out.astype(np.float64) - exp) <= bound)
+
+
+def test_gemv_closed_forms():
+    # A row-selection matrix (m != k): out[i] = x[perm[i]] exactly; reading the
+    # weight transposed or with the wrong row stride picks other entries.
+    m, k = 40, 24
+    g = rng(930)
+    perm = g.integers(0, k, m)
+    w = np.zeros((m, k), np.float16)
+    w[np.arange(m), perm] = 1.0
+    x = normal_f16(g, k)
+    assert np.array_equal(oracle.gemv_f16(w, x), x[perm])
+    # Linearity: scaling x by a power of two scales the output exactly.
+    w = normal_f16(g, (m, 256), 0.0625)
+    x = normal_f16(g, 256)
+    assert np.array_equal(oracle.gemv_f16(w, x * np.float16(4)),
+                          (oracle.gemv_f16(w, x).astype(np.float32) * 4).astype(np.float16))
+    # All-ones weight: the sum of x (exact in f32 for these small integers).
+    xi = g.integers(-8, 9, 512).astype(np.float16)
+    assert oracle.gemv_f16(np.ones((3, 512), np.float16), xi)[0] == np.float16(xi.astype(np.float64).sum())
+
+
+def test_argmax_against_numpy():
+    g = rng(940)
+    for n in (1, 7, 2048, 2049, 151936):
+        lg = normal_f16(g, n, 4.0)
+        assert oracle.argmax_f16(lg) == int(np.argmax(lg))
+    n = 151936
+    lg = normal_f16(g, n)
+    lg[[5000, 90000, 150000]] = np.float16(30.0)   # ties across blocks: lowest index
+    assert oracle.argmax_f16(lg) == 5000
+    lg[4000] = np.float16(np.nan)                  # NaN is never chosen
+    lg[100] = np.float16(-np.inf)
+    assert oracle.argmax_f16(lg) == 5000 == int(np.nanargmax(lg))
+    assert oracle.argmax_f16(np.full(3000, -np.inf, np.float16)) == 0
+    assert oracle.argmax_f16(np.full(3000, np.nan, np.float16)) == 0
+    nanfirst = np.array([np.nan, 1.0, 3.0, 3.0, 2.0], np.float16)
+    assert oracle.argmax_f16(nanfirst) == 2
