@@ -40,7 +40,8 @@ __all__ = [
     "qk_norm_rope_kv_decode", "attend_prefill", "fmha_decode_gqa_split",
     "splitk_reduce_merge", "decode_fused", "attend_prefill_split", "prefill_split_scratch",
     "prefill_splitk_reduce_merge", "add_rms_norm_decode", "gemv_f16", "argmax_scratch",
-    "argmax_f16", "decode_scratch", "decode_counters",
+    "argmax_f16", "embed_rms_norm_decode", "silu_mul", "Qwen3DecodeRunner", "QWEN3_LAYER_KEYS",
+    "decode_scratch", "decode_counters",
     "pick_num_splits", "DecodeGraphRunner",
     "HEAD_DIM", "ATTN_BN_DECODE",
 ]
@@ -322,6 +323,133 @@ def argmax_f16(logits, block_max, block_idx, token):
     _check(lib().grout_argmax_f16(_ptr(logits), _ptr(block_max), _ptr(block_idx), _ptr(token),
                                   logits.numel(), _stream()), "argmax_f16")
     return token
+
+
+def embed_rms_norm_decode(token, table, weight, out, residual_out, eps: float):
+    """embedding_batch_f16 + rms_norm_f16 (src/kernels.rs:693-711, 304-344) for the
+    device token id token[0]: residual_out = table[token], out = RMSNorm(row) * weight."""
+    _ensure(table.dim() == 2, f"table must be [vocab, n], got {list(table.shape)}")
+    vocab, n = table.shape
+    for t, nm in ((weight, "weight"), (out, "out"), (residual_out, "residual_out")):
+        _ensure(t.numel() == n, f"{nm} must have {n} elements, got {t.numel()}")
+    for t, nm in ((table, "table"), (weight, "weight"), (out, "out"),
+                  (residual_out, "residual_out")):
+        _f16(t, nm)
+    _check(lib().grout_embed_rms_norm_decode(_ptr(token), _ptr(table), vocab, _ptr(weight),
+                                             _ptr(out), _ptr(residual_out), float(eps), n,
+                                             _stream()), "embed_rms_norm_decode")
+    return out, residual_out
+
+
+def silu_mul(gate, up, out):
+    """silu_mul_2d_f16 (src/kernels.rs:271-301): out = sigmoid(gate) * gate * up."""
+    n = out.numel()
+    _ensure(gate.numel() == n and up.numel() == n, "gate, up and out must have equal sizes")
+    for t, nm in ((gate, "gate"), (up, "up"), (out, "out")):
+        _f16(t, nm)
+    _check(lib().grout_silu_mul_f16(_ptr(gate), _ptr(up), _ptr(out), n, _stream()), "silu_mul")
+    return out
+
+
+QWEN3_LAYER_KEYS = ("input_norm", "qkv_proj", "q_norm", "k_norm", "o_proj", "post_attn_norm",
+                    "gate_up_proj", "down_proj", "k_cache", "v_cache")
+
+
+class Qwen3DecodeRunner:
+    """DecodeCudaGraphRunner (src/model.rs:318-493) with the graph of
+    src/model.rs:3118-3648: the whole Qwen3 decode step (embedding, every
+    layer's norms, GEMVs, attention and MLP, final norm, lm_head, greedy
+    argmax) captured once into a hipGraph over borrowed weights and caches.
+
+    `layers` holds one dict per layer with the keys of QWEN3_LAYER_KEYS;
+    `token` and `position` are device int32[1] tensors (the step reads the
+    token and writes the next one in place), `logits` a device f16[vocab]."""
+
+    def __init__(self, *, layers, embed_tokens, final_norm, lm_head, inv_freq, token, position,
+                 logits, num_q_heads: int, num_kv_heads: int, eps: float,
+                 qk_scale_f16_bits: int, num_splits: int | None = None,
+                 block_n: int = ATTN_BN_DECODE, prime_position: int = 0, stream=None):
+        torch = _torch()
+        _ensure(len(layers) >= 1, "at least one layer")
+        _ensure(embed_tokens.dim() == 2, "embed_tokens must be [vocab, hidden]")
+        vocab, hidden = embed_tokens.shape
+        hq, hkv = num_q_heads, num_kv_heads
+        _ensure(hq > 0 and hkv > 0 and hq % hkv == 0,
+                f"num_q_heads {hq} must be a multiple of num_kv_heads {hkv}")
+        d = HEAD_DIM
+        inter = layers[0]["down_proj"].shape[1]
+        max_seq = layers[0]["k_cache"].shape[1]
+        shapes = {"input_norm": (hidden,), "qkv_proj": ((hq + 2 * hkv) * d, hidden),
+                  "q_norm": (d,), "k_norm": (d,), "o_proj": (hidden, hq * d),
+                  "post_attn_norm": (hidden,), "gate_up_proj": (2 * inter, hidden),
+                  "down_proj": (hidden, inter), "k_cache": (hkv, max_seq, d),
+                  "v_cache": (hkv, max_seq, d)}
+        for i, L in enumerate(layers):
+            for key in QWEN3_LAYER_KEYS:
+                _ensure(key in L, f"layer {i} has no {key}")
+                _ensure(tuple(L[key].shape) == shapes[key],
+                        f"layer {i} {key} shape {list(L[key].shape)} != {list(shapes[key])}")
+                _f16(L[key], f"layer {i} {key}")
+        _ensure(tuple(lm_head.shape) == (vocab, hidden), "lm_head must be [vocab, hidden]")
+        _ensure(final_norm.numel() == hidden and logits.numel() == vocab,
+                "final_norm [hidden] and logits [vocab] expected")
+        if num_splits is None:
+            num_splits = pick_num_splits(max_seq, hkv, block_n)
+        self._layers = (_lib.Qwen3Layer * len(layers))(*[
+            _lib.Qwen3Layer(**{key: _ptr(L[key]) for key in QWEN3_LAYER_KEYS}) for L in layers])
+        M = _lib.Qwen3Model(
+            num_layers=len(layers), hidden=hidden, intermediate=inter, vocab=vocab,
+            num_q_heads=hq, num_kv_heads=hkv, head_dim=d, max_seq_len=max_seq, block_n=block_n,
+            num_splits=num_splits, eps=float(eps), qk_scale_f16=int(qk_scale_f16_bits),
+            layers=self._layers, embed_tokens=_ptr(embed_tokens), final_norm=_ptr(final_norm),
+            lm_head=_ptr(lm_head), inv_freq=_ptr(inv_freq), token=_ptr(token),
+            d_position=_ptr(position), logits=_ptr(logits), workspace=None)
+        nbytes = int(lib().grout_qwen3_workspace_bytes(ctypes.byref(M)))
+        _check(nbytes if nbytes < 0 else 0, "qwen3_workspace_bytes")
+        self.workspace = torch.empty((nbytes,), dtype=torch.uint8, device=embed_tokens.device)
+        M.workspace = self.workspace.data_ptr()
+        _ensure(M.workspace % 256 == 0, "workspace must be 256-byte aligned")
+        self._model = M
+        self.num_splits = num_splits
+        self._keep = (layers, embed_tokens, final_norm, lm_head, inv_freq, token, position, logits)
+        self.stream = stream if stream is not None else torch.cuda.Stream()
+        torch.cuda.current_stream().synchronize()  # caller's buffers are ready
+        h = ctypes.c_void_p()
+        _check(lib().grout_qwen3_runner_create(ctypes.byref(M), int(prime_position),
+                                               self.stream.cuda_stream, ctypes.byref(h)),
+               "qwen3_runner_create")
+        self._h = h
+
+    def seed_token(self, token: int):
+        _check(lib().grout_qwen3_runner_seed_token(self._h, int(token)), "qwen3_seed_token")
+
+    def step(self, position: int) -> int:
+        """launch_step: one replay at `position`; returns the token it picked."""
+        out = ctypes.c_uint32()
+        _check(lib().grout_qwen3_runner_step(self._h, int(position), ctypes.byref(out)),
+               "qwen3_runner_step")
+        return int(out.value)
+
+    def run(self, first_position: int, count: int):
+        """`count` replays from `first_position`, each embedding the previous token."""
+        _check(lib().grout_qwen3_runner_run(self._h, int(first_position), int(count)),
+               "qwen3_runner_run")
+
+    def eager_step(self):
+        """The same step launched op by op on the runner's stream (no graph)."""
+        _check(lib().grout_qwen3_decode_step(ctypes.byref(self._model), self.stream.cuda_stream),
+               "qwen3_decode_step")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _check(lib().grout_qwen3_runner_destroy(self._h), "qwen3_runner_destroy")
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def pick_num_splits(max_context: int, num_kv_heads: int, block_n: int = ATTN_BN_DECODE,

@@ -47,6 +47,27 @@ class DecodeLayer(ctypes.Structure):
     ]
 
 
+class Qwen3Layer(ctypes.Structure):
+    """struct grout_qwen3_layer."""
+    _fields_ = [
+        ("input_norm", c_vp), ("qkv_proj", c_vp), ("q_norm", c_vp), ("k_norm", c_vp),
+        ("o_proj", c_vp), ("post_attn_norm", c_vp), ("gate_up_proj", c_vp),
+        ("down_proj", c_vp), ("k_cache", c_vp), ("v_cache", c_vp),
+    ]
+
+
+class Qwen3Model(ctypes.Structure):
+    """struct grout_qwen3_model."""
+    _fields_ = [
+        ("num_layers", c_i32), ("hidden", c_i32), ("intermediate", c_i32), ("vocab", c_i32),
+        ("num_q_heads", c_i32), ("num_kv_heads", c_i32), ("head_dim", c_i32),
+        ("max_seq_len", c_i32), ("block_n", c_i32), ("num_splits", c_i32), ("eps", c_f32),
+        ("qk_scale_f16", c_u16), ("layers", ctypes.POINTER(Qwen3Layer)),
+        ("embed_tokens", c_vp), ("final_norm", c_vp), ("lm_head", c_vp), ("inv_freq", c_vp),
+        ("token", c_vp), ("d_position", c_vp), ("logits", c_vp), ("workspace", c_vp),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "grout_status_string": (ctypes.c_char_p, [c_i32]),
@@ -64,6 +85,17 @@ SIGNATURES = {
     "grout_gemv_f16": (c_i32, [c_vp] * 3 + [c_i32] * 2 + [c_vp]),
     "grout_argmax_blocks": (c_i32, [c_i32]),
     "grout_argmax_f16": (c_i32, [c_vp] * 4 + [c_i32, c_vp]),
+    "grout_embed_rms_norm_decode": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32,
+                                            c_vp]),
+    "grout_silu_mul_f16": (c_i32, [c_vp] * 3 + [c_i32, c_vp]),
+    "grout_qwen3_workspace_bytes": (c_i64, [ctypes.POINTER(Qwen3Model)]),
+    "grout_qwen3_decode_step": (c_i32, [ctypes.POINTER(Qwen3Model), c_vp]),
+    "grout_qwen3_runner_create": (
+        c_i32, [ctypes.POINTER(Qwen3Model), c_u32, c_vp, ctypes.POINTER(c_vp)]),
+    "grout_qwen3_runner_seed_token": (c_i32, [c_vp, c_u32]),
+    "grout_qwen3_runner_step": (c_i32, [c_vp, c_u32, ctypes.POINTER(c_u32)]),
+    "grout_qwen3_runner_run": (c_i32, [c_vp, c_u32, c_i32]),
+    "grout_qwen3_runner_destroy": (c_i32, [c_vp]),
     "grout_attn_decode_split": (
         c_i32, [c_vp] * 5 + [c_u16, c_vp] + [c_i32] * 6 + [c_vp]),
     "grout_attn_decode_merge": (c_i32, [c_vp] * 3 + [c_i32] * 4 + [c_vp]),

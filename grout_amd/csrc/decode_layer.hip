@@ -37,12 +37,24 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return v;
 }
 
-__global__ __launch_bounds__(kNormThreads) void add_rms_norm_decode_kernel(
+// kEmbed = false: the row is residual + x (add_rms_norm_decode_raw_f16).
+// kEmbed = true: the row is embedding row *token of `residual` (the table,
+// [vocab, n]) and x is absent: embedding_batch_f16 followed by rms_norm_f16
+// (src/kernels.rs:693-711, :304-344), with residual_out receiving the row.
+template <bool kEmbed>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_decode_kernel(
     const uint16_t* residual, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    uint16_t* __restrict__ out, uint16_t* residual_out, float eps, int n) {
+    uint16_t* __restrict__ out, uint16_t* residual_out, float eps, int n,
+    const uint32_t* __restrict__ token, uint32_t vocab) {
     // residual_out may be residual itself (the decode graph updates the
     // residual stream in place): each thread reads its chunks before the
     // barrier and writes the same chunks after it.
+    if constexpr (kEmbed) {
+        // A token id past the table (never produced by the argmax; only a bad
+        // initial value) reads the last row instead of faulting.
+        const uint32_t t = min(*token, vocab - 1u);
+        residual += static_cast<int64_t>(t) * n;
+    }
     __shared__ float red[kNormThreads / kWave];
     const int tid = threadIdx.x;
     float c[kNormChunks][8];
@@ -52,12 +64,17 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_decode_kernel(
         const int i = (tid + k * kNormThreads) * 8;
         if (i < n) {
             const half8_t r8 = load_half8(residual + i);
-            const half8_t x8 = load_half8(x + i);
+            if constexpr (kEmbed) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                c[k][e] = static_cast<float>(r8[e]) + static_cast<float>(x8[e]);
-                ss += c[k][e] * c[k][e];
+                for (int e = 0; e < 8; ++e) c[k][e] = static_cast<float>(r8[e]);
+            } else {
+                const half8_t x8 = load_half8(x + i);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    c[k][e] = static_cast<float>(r8[e]) + static_cast<float>(x8[e]);
             }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += c[k][e] * c[k][e];
         }
     }
     ss = wave_sum_f32(ss);
@@ -83,6 +100,30 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_decode_kernel(
             store_half8(residual_out + i, rs);
         }
     }
+}
+
+// -------------------------------------------------------------- SiLU * up --
+
+constexpr int kPointwiseThreads = 256;
+
+// silu_mul_2d_f16 (src/kernels.rs:271-301): out = f16(sigmoid(g) * g * u) in
+// f32 with sigmoid(g) = 1 / (1 + exp(-g)); 8 elements per thread.
+__global__ __launch_bounds__(kPointwiseThreads) void silu_mul_kernel(
+    const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, uint16_t* __restrict__ out,
+    int n) {
+#pragma clang fp contract(off)
+    const int i = (static_cast<int>(blockIdx.x) * kPointwiseThreads + static_cast<int>(threadIdx.x)) * 8;
+    if (i >= n) return;
+    const half8_t g8 = load_half8(gate + i);
+    const half8_t u8 = load_half8(up + i);
+    half8_t o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float g = static_cast<float>(g8[e]);
+        const float sig = 1.0f / (1.0f + expf(-g));
+        o[e] = static_cast<half_t>((sig * g) * static_cast<float>(u8[e]));
+    }
+    store_half8(out + i, o);
 }
 
 // ------------------------------------------------------------------ GEMV --
@@ -271,8 +312,38 @@ extern "C" int32_t grout_add_rms_norm_decode(const uint16_t* residual, const uin
     GROUT_REQUIRE_PTR(residual_out);
     GROUT_REQUIRE(n >= 8 && n % 8 == 0 && n <= kNormMaxN, GROUT_ERR_ARG);
     GROUT_REQUIRE(eps >= 0.0f && eps < 1.0e30f, GROUT_ERR_ARG);
-    hipLaunchKernelGGL(add_rms_norm_decode_kernel, dim3(1), dim3(kNormThreads), 0, to_hip(stream),
-                       residual, x, weight, out, residual_out, eps, n);
+    hipLaunchKernelGGL(rms_norm_decode_kernel<false>, dim3(1), dim3(kNormThreads), 0,
+                       to_hip(stream), residual, x, weight, out, residual_out, eps, n, nullptr, 0u);
+    return launch_status();
+}
+
+extern "C" int32_t grout_embed_rms_norm_decode(const uint32_t* token, const uint16_t* table,
+                                               int32_t vocab, const uint16_t* weight,
+                                               uint16_t* out, uint16_t* residual_out, float eps,
+                                               int32_t n, grout_stream_t stream) {
+    GROUT_REQUIRE(token != nullptr, GROUT_ERR_NULL_POINTER);
+    GROUT_REQUIRE((reinterpret_cast<uintptr_t>(token) & 3u) == 0, GROUT_ERR_ALIGNMENT);
+    GROUT_REQUIRE_PTR(table);
+    GROUT_REQUIRE_PTR(weight);
+    GROUT_REQUIRE_PTR(out);
+    GROUT_REQUIRE_PTR(residual_out);
+    GROUT_REQUIRE(n >= 8 && n % 8 == 0 && n <= kNormMaxN && vocab >= 1, GROUT_ERR_ARG);
+    GROUT_REQUIRE(eps >= 0.0f && eps < 1.0e30f, GROUT_ERR_ARG);
+    hipLaunchKernelGGL(rms_norm_decode_kernel<true>, dim3(1), dim3(kNormThreads), 0,
+                       to_hip(stream), table, nullptr, weight, out, residual_out, eps, n, token,
+                       static_cast<uint32_t>(vocab));
+    return launch_status();
+}
+
+extern "C" int32_t grout_silu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out,
+                                      int32_t n, grout_stream_t stream) {
+    GROUT_REQUIRE_PTR(gate);
+    GROUT_REQUIRE_PTR(up);
+    GROUT_REQUIRE_PTR(out);
+    GROUT_REQUIRE(n >= 8 && n % 8 == 0, GROUT_ERR_ARG);
+    const unsigned blocks = static_cast<unsigned>((n / 8 + kPointwiseThreads - 1) / kPointwiseThreads);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(kPointwiseThreads), 0, to_hip(stream),
+                       gate, up, out, n);
     return launch_status();
 }
 

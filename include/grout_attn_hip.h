@@ -192,11 +192,26 @@ int64_t grout_attn_prefill_split_lse_bytes(int32_t num_q_heads, int32_t q_len, i
  * in the decode graph (src/model.rs:3151-3163, 3513-3526): for one row of n,
  * combined = f32(residual) + f32(x); inv = 1/sqrt(sum(combined^2)/n + eps);
  * out = f16(combined*inv*weight); residual_out = f16(combined).
- * n a multiple of 8, at most 32768; buffers 16-byte aligned, out and
- * residual_out may not alias the inputs. */
+ * n a multiple of 8, at most 32768; buffers 16-byte aligned; residual_out
+ * may be residual itself, out may alias no input. */
 int32_t grout_add_rms_norm_decode(const uint16_t* residual, const uint16_t* x,
                                   const uint16_t* weight, uint16_t* out, uint16_t* residual_out,
                                   float eps, int32_t n, grout_stream_t stream);
+
+/* Replaces embedding_batch_f16 + rms_norm_f16 at the head of the decode graph
+ * (src/kernels.rs:693-711, 304-344; src/model.rs:3120-3149) in one launch:
+ * row = table[*token] ([vocab, n] f16), residual_out = row,
+ * out = f16(row * 1/sqrt(sum(row^2)/n + eps) * weight).  *token is read on
+ * the device (the previous step's argmax); an id >= vocab reads row vocab-1. */
+int32_t grout_embed_rms_norm_decode(const uint32_t* token, const uint16_t* table, int32_t vocab,
+                                    const uint16_t* weight, uint16_t* out, uint16_t* residual_out,
+                                    float eps, int32_t n, grout_stream_t stream);
+
+/* Replaces silu_mul_2d_f16 (src/kernels.rs:271-301; src/model.rs:3556-3565):
+ * out[i] = f16(sigmoid(g) * g * u), g = f32(gate[i]), u = f32(up[i]),
+ * sigmoid(g) = 1 / (1 + exp(-g)).  n a multiple of 8; 16-byte aligned. */
+int32_t grout_silu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int32_t n,
+                           grout_stream_t stream);
 
 /* Replaces the cuBLAS GemvInPlace nodes of the decode graph (src/cublas.rs:572-607:
  * cublasGemmEx(OP_T, OP_N, m, 1, k) on a row-major [m, k] f16 weight):
@@ -353,6 +368,79 @@ int32_t grout_decode_runner_run(grout_decode_runner* runner, uint32_t first_posi
  * stay valid for the captured graph.  Synchronises the runner's stream. */
 int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner);
 int32_t grout_decode_runner_destroy(grout_decode_runner* runner);
+
+/* ------------------------------------ Qwen3 decode token step (N1) */
+/* The whole decode graph of DecodeCudaGraphRunner (src/model.rs:3118-3648)
+ * on this library's kernels: embedding + input RMSNorm of *token, then per
+ * layer [add + input RMSNorm] -> qkv GEMV -> fused QK norm/RoPE/KV write +
+ * split-K decode + merge -> o_proj GEMV -> add + post-attention RMSNorm ->
+ * gate_up GEMV -> SiLU * up -> down GEMV; then the final add + RMSNorm, the
+ * lm_head GEMV into `logits` and the greedy argmax into *token, which the
+ * next step's embedding reads.  The last layer's attention advances
+ * *d_position.  Weights, caches and buffers are borrowed. */
+typedef struct grout_qwen3_layer {
+    const uint16_t* input_norm;      /* [hidden] input_layernorm */
+    const uint16_t* qkv_proj;        /* [(Hq + 2*Hkv)*128, hidden], rows Q | K | V
+                                        (src/model.rs:1390-1401) */
+    const uint16_t* q_norm;          /* [128] */
+    const uint16_t* k_norm;          /* [128] */
+    const uint16_t* o_proj;          /* [hidden, Hq*128] */
+    const uint16_t* post_attn_norm;  /* [hidden] post_attention_layernorm */
+    const uint16_t* gate_up_proj;    /* [2*intermediate, hidden], rows gate | up */
+    const uint16_t* down_proj;       /* [hidden, intermediate] */
+    uint16_t* k_cache;               /* [Hkv, max_seq_len, 128] */
+    uint16_t* v_cache;               /* [Hkv, max_seq_len, 128] */
+} grout_qwen3_layer;
+
+typedef struct grout_qwen3_model {
+    int32_t num_layers;
+    int32_t hidden;          /* multiple of 8, <= 32768 */
+    int32_t intermediate;    /* multiple of 8, <= 32768 */
+    int32_t vocab;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;        /* 128 */
+    int32_t max_seq_len;
+    int32_t block_n;         /* decode KV tile (32) */
+    int32_t num_splits;      /* grout_attn_decode_pick_splits */
+    float eps;
+    uint16_t qk_scale_f16;
+    const grout_qwen3_layer* layers;  /* num_layers entries (copied by the runner) */
+    const uint16_t* embed_tokens;     /* [vocab, hidden] */
+    const uint16_t* final_norm;       /* [hidden] */
+    const uint16_t* lm_head;          /* [vocab, hidden] (embed_tokens when tied) */
+    const float* inv_freq;            /* [64] grout_build_inv_freq */
+    uint32_t* token;                  /* device u32: this step's input, next step's token */
+    uint32_t* d_position;             /* device u32 */
+    uint16_t* logits;                 /* [vocab] f16 */
+    void* workspace;                  /* grout_qwen3_workspace_bytes, 256-byte aligned */
+} grout_qwen3_model;
+
+/* Bytes of activations + scratch the step needs (< 0: invalid model). */
+int64_t grout_qwen3_workspace_bytes(const grout_qwen3_model* model);
+/* One eager step in stream order at *d_position (the sequence the graph
+ * holds).  The workspace's attention counters must be zero before the first
+ * step on it (grout_qwen3_runner_create clears them). */
+int32_t grout_qwen3_decode_step(const grout_qwen3_model* model, grout_stream_t stream);
+
+typedef struct grout_qwen3_runner grout_qwen3_runner;
+/* Clears the counters, runs one eager prime step at prime_position (it writes
+ * the caches there, replaces *token and advances the position, as any step),
+ * then captures the step into a hipGraph. */
+int32_t grout_qwen3_runner_create(const grout_qwen3_model* model, uint32_t prime_position,
+                                  grout_stream_t stream, grout_qwen3_runner** runner);
+/* seed_token (src/model.rs:343-356): stream-ordered write of *token. */
+int32_t grout_qwen3_runner_seed_token(grout_qwen3_runner* runner, uint32_t token);
+/* launch_step (src/model.rs:363-403): position write unless the previous step
+ * left it, graph replay; when token_out is not NULL, the new token is copied
+ * back and the stream synchronised. */
+int32_t grout_qwen3_runner_step(grout_qwen3_runner* runner, uint32_t position,
+                                uint32_t* token_out);
+/* `count` consecutive steps from first_position without host round trips
+ * (each step embeds the token the previous one picked).  No host sync. */
+int32_t grout_qwen3_runner_run(grout_qwen3_runner* runner, uint32_t first_position,
+                               int32_t count);
+int32_t grout_qwen3_runner_destroy(grout_qwen3_runner* runner);
 
 #ifdef __cplusplus
 }

@@ -65,6 +65,7 @@ def lib():
         L.go_gemv_f16.argtypes = [_u16p] * 3 + [_i32] * 3
         L.go_argmax_f16.restype = ctypes.c_uint32
         L.go_argmax_f16.argtypes = [_u16p, _i32]
+        L.go_silu_mul.argtypes = [_u16p] * 3 + [_i32]
         _lib = L
     return _lib
 
@@ -224,3 +225,46 @@ def gemv_f16(w, x, nthreads: int = 0) -> np.ndarray:
 
 def argmax_f16(logits) -> int:
     return int(lib().go_argmax_f16(_u16(logits), logits.shape[0]))
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    out = np.zeros(gate.shape[0], dtype=np.float16)
+    lib().go_silu_mul(_u16(gate), _u16(up), _u16(out), gate.shape[0])
+    return out
+
+
+def qwen3_decode_step(model: dict, token: int, position: int, block_n: int, num_splits: int):
+    """One decode token step of src/model.rs:3118-3648, composed of this
+    oracle's ops in the graph's order.  `model` holds numpy f16 arrays
+    (embed_tokens, final_norm, lm_head, inv_freq (f32), layers: list of dicts
+    with input_norm, qkv_proj, q_norm, k_norm, o_proj, post_attn_norm,
+    gate_up_proj, down_proj, k_cache, v_cache) and eps, qk_scale_f16_bits,
+    num_q_heads, num_kv_heads.  Writes the caches at `position` in place.
+    Returns (logits f16 [vocab], next token)."""
+    hq, hkv, eps = model["num_q_heads"], model["num_kv_heads"], model["eps"]
+    D = 128
+    G = hq // hkv
+    row = model["embed_tokens"][token]                       # :3120-3128
+    zero = np.zeros_like(row)
+    normed, hidden = add_rms_norm(row, zero, model["layers"][0]["input_norm"], eps)  # :3133-3149
+    hidden_after_attn = ff_down = None
+    for li, L in enumerate(model["layers"]):
+        if li > 0:                                           # :3151-3163
+            normed, hidden = add_rms_norm(hidden_after_attn, ff_down, L["input_norm"], eps)
+        qkv = gemv_f16(L["qkv_proj"], normed)                # :3170-3176
+        q_out = np.zeros(((hq + hkv) * D,), np.float16)
+        qk_norm_rope_kv_decode(qkv, L["q_norm"], L["k_norm"], model["inv_freq"], q_out,
+                               L["k_cache"], L["v_cache"], position, eps, hq, hkv)
+        qg = q_out[:hq * D].reshape(hkv, G, D)
+        att, lse = attn_decode_split(qg, L["k_cache"], L["v_cache"], model["qk_scale_f16_bits"],
+                                     position, block_n, num_splits)
+        attn_out = attn_decode_merge(att, lse, G).reshape(-1)
+        attn_proj = gemv_f16(L["o_proj"], attn_out)          # :3505-3511
+        normed, hidden_after_attn = add_rms_norm(hidden, attn_proj, L["post_attn_norm"], eps)
+        gate_up = gemv_f16(L["gate_up_proj"], normed)        # :3529-3535
+        inter = gate_up.shape[0] // 2
+        ff = silu_mul(gate_up[:inter], gate_up[inter:])      # :3556-3565
+        ff_down = gemv_f16(L["down_proj"], ff)               # :3568-3574
+    normed, hidden = add_rms_norm(hidden_after_attn, ff_down, model["final_norm"], eps)
+    logits = gemv_f16(model["lm_head"], normed)              # :3612-3620
+    return logits, argmax_f16(logits)                        # :3622-3640

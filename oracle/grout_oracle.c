@@ -667,3 +667,13 @@ uint32_t go_argmax_f16(const uint16_t* logits, int32_t n) {
     }
     return best < 0 ? 0u : (uint32_t)best;
 }
+
+/* src/kernels.rs:271-301 silu_mul_2d_f16: y = f16((sigmoid(g) * g) * u) in
+ * f32, sigmoid(g) = 1 / (1 + exp(-g)) (:288-293). */
+void go_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int32_t n) {
+    for (int32_t i = 0; i < n; ++i) {
+        const float g = h2f(gate[i]);
+        const float sig = 1.0f / (1.0f + expf(-g));
+        out[i] = go_f32_to_f16((sig * g) * h2f(up[i]));
+    }
+}

@@ -112,6 +112,9 @@ void go_gemv_f16(const uint16_t* w, const uint16_t* x, uint16_t* out, int32_t m,
 /* src/kernels.rs:345-505 two-stage greedy argmax: lowest index of the largest logit. */
 uint32_t go_argmax_f16(const uint16_t* logits, int32_t n);
 
+/* src/kernels.rs:271-301 silu_mul_2d_f16. */
+void go_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int32_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,3 +57,39 @@ def qk_scale_f16_bits() -> int:
 
 def f16_bits_to_f32(bits: int) -> float:
     return float(np.array([bits], dtype=np.uint16).view(np.float16)[0])
+
+
+def qwen3_tiny_model(seed_offset: int, layers: int = 2, hidden: int = 256, hq: int = 4,
+                     hkv: int = 2, inter: int = 512, vocab: int = 1000, max_seq: int = 64,
+                     filled: int = 20, logit_scale: float = 4.0) -> dict:
+    """A small random Qwen3-shaped decode model (numpy, f16): weights scaled
+    so activations stay O(1), KV caches holding N(0,1) rows at positions
+    [0, filled) and zeros after."""
+    g = rng(seed_offset)
+
+    def lin(m, k, scale=1.0):
+        return normal_f16(g, (m, k), scale / np.sqrt(k))
+
+    def nw(n):
+        return (1.0 + 0.1 * g.standard_normal(n, dtype=np.float32)).astype(np.float16)
+
+    def cache():
+        c = np.zeros((hkv, max_seq, D), np.float16)
+        c[:, :filled] = normal_f16(g, (hkv, filled, D))
+        return c
+
+    m = {"num_q_heads": hq, "num_kv_heads": hkv, "eps": EPS,
+         "qk_scale_f16_bits": qk_scale_f16_bits(), "layers": []}
+    for _ in range(layers):
+        m["layers"].append({
+            "input_norm": nw(hidden), "qkv_proj": lin((hq + 2 * hkv) * D, hidden),
+            "q_norm": nw(D), "k_norm": nw(D), "o_proj": lin(hidden, hq * D),
+            "post_attn_norm": nw(hidden), "gate_up_proj": lin(2 * inter, hidden),
+            "down_proj": lin(hidden, inter), "k_cache": cache(), "v_cache": cache()})
+    m["embed_tokens"] = normal_f16(g, (vocab, hidden))
+    m["final_norm"] = nw(hidden)
+    m["lm_head"] = lin(vocab, hidden, logit_scale)
+    import oracle
+
+    m["inv_freq"] = oracle.build_inv_freq(THETA)
+    return m

@@ -225,6 +225,68 @@ def test_decode_layer_checks(L):
     assert a(A, A, A, A, 0, S) == -9
 
 
+def test_token_step_op_checks(L):
+    e = L.grout_embed_rms_norm_decode
+    # token, table, vocab, weight, out, residual_out, eps, n, stream
+    assert e(0, A, 10, A, A, A, 1e-6, 64, S) == -1
+    assert e(A + 2, A, 10, A, A, A, 1e-6, 64, S) == -2    # token needs 4-byte alignment
+    assert e(A, U, 10, A, A, A, 1e-6, 64, S) == -2
+    assert e(A, A, 0, A, A, A, 1e-6, 64, S) == -9
+    assert e(A, A, 10, A, A, A, 1e-6, 60, S) == -9
+    s = L.grout_silu_mul_f16
+    assert s(A, 0, A, 64, S) == -1
+    assert s(A, A, U, 64, S) == -2
+    assert s(A, A, A, 12, S) == -9
+    assert s(A, A, A, 0, S) == -9
+
+
+def _qwen3_model(**over):
+    import ctypes
+
+    from grout_amd import _lib
+
+    layers = (_lib.Qwen3Layer * 2)(*[_lib.Qwen3Layer(*([A] * 10)) for _ in range(2)])
+    kw = dict(num_layers=2, hidden=256, intermediate=512, vocab=1000, num_q_heads=4,
+              num_kv_heads=2, head_dim=128, max_seq_len=64, block_n=32, num_splits=3,
+              eps=1e-6, qk_scale_f16=0x2DA8, layers=layers, embed_tokens=A, final_norm=A,
+              lm_head=A, inv_freq=A, token=A, d_position=A, logits=A, workspace=A)
+    kw.update(over)
+    m = _lib.Qwen3Model(**kw)
+    m._keep = layers
+    return ctypes.byref(m)
+
+
+def test_token_step_runner_checks(L):
+    import ctypes
+
+    from grout_amd import _lib
+
+    ws = L.grout_qwen3_workspace_bytes
+    assert ws(None) == -1
+    n = ws(_qwen3_model())
+    # hidden x3 + qkv + q_out + attn_out + attn_proj + gate_up + ff + ff_down
+    # + partials + lse + counters + argmax blocks, each rounded up to 256 bytes.
+    assert n > 2 * (3 * 256 + 8 * 128 + 6 * 128 + 4 * 128 + 256 + 1024 + 512 + 256)
+    assert n % 256 == 0
+    assert ws(_qwen3_model(num_layers=0)) == -9
+    assert ws(_qwen3_model(head_dim=64)) == -3
+    assert ws(_qwen3_model(num_q_heads=5)) == -4
+    assert ws(_qwen3_model(hidden=260)) == -9
+    assert ws(_qwen3_model(num_splits=0)) == -8
+    assert ws(_qwen3_model(layers=None)) == -1
+    st = L.grout_qwen3_decode_step
+    assert st(_qwen3_model(workspace=None), S) == -1
+    assert st(_qwen3_model(workspace=A + 16), S) == -2      # workspace needs 256-byte alignment
+    h = ctypes.c_void_p()
+    assert L.grout_qwen3_runner_create(_qwen3_model(), 0, S, ctypes.byref(h)) == -10  # null stream
+    assert L.grout_qwen3_runner_create(_qwen3_model(), 64, A, ctypes.byref(h)) == -5
+    assert L.grout_qwen3_runner_step(None, 0, None) == -10
+    assert L.grout_qwen3_runner_run(None, 0, 1) == -10
+    assert L.grout_qwen3_runner_seed_token(None, 0) == -10
+    assert L.grout_qwen3_runner_destroy(None) == 0
+    assert _lib.SIGNATURES["grout_qwen3_runner_create"][0] is ctypes.c_int32
+
+
 def test_graph_handle_checks(L):
     assert L.grout_graph_begin(None) == -10
     assert L.grout_graph_launch(None, None) == -10

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import oracle
-from tests._util import D, EPS, THETA, f16_ulp_diff, norm_weight, normal_f16, qk_scale_f16_bits, rng
+from tests._util import (D, EPS, THETA, f16_ulp_diff, norm_weight, normal_f16, qk_scale_f16_bits,
+                         qwen3_tiny_model, rng)
 
 SCALE = 1.0 / math.sqrt(D)
 
@@ -559,3 +560,81 @@ def test_argmax_against_numpy():
     assert oracle.argmax_f16(np.full(3000, np.nan, np.float16)) == 0
     nanfirst = np.array([np.nan, 1.0, 3.0, 3.0, 2.0], np.float16)
     assert oracle.argmax_f16(nanfirst) == 2
+
+
+def test_silu_mul_against_float64():
+    g = rng(950)
+    gate = np.concatenate([normal_f16(g, 20000, 4.0),
+                           np.float16([0.0, -0.0, 30.0, -30.0, 11.0, -17.0, 65504, -65504])])
+    up = normal_f16(g, gate.shape[0])
+    out = oracle.silu_mul(gate, up)
+    g64, u64 = gate.astype(np.float64), up.astype(np.float64)
+    with np.errstate(over="ignore"):
+        exp = g64 / (1.0 + np.exp(-g64)) * u64
+    finite = np.isfinite(exp) & (np.abs(exp) < 65504)
+    assert np.all(f16_ulp_diff(out[finite], exp[finite].astype(np.float16)) <= 1)
+    assert np.mean(out[finite] == exp[finite].astype(np.float16)) > 0.999
+    # silu(0) = 0, silu(g) -> g for large g, -> 0 for very negative g.
+    one = np.ones(4, np.float16)
+    assert np.array_equal(oracle.silu_mul(np.float16([0.0, 30.0, -30.0, -100.0]), one),
+                          np.float16([0.0, 30.0, -0.0, -0.0]))
+
+
+def _qwen3_step_f64(m, token, pos):
+    """Independent float64 Qwen3 decode step (no f16 intermediates): RMSNorm,
+    merged QKV, per-head QK norm + RoPE, causal attention over [0, pos],
+    residual adds, SwiGLU MLP, final norm, lm_head.  Returns logits and the
+    updated caches."""
+    f = lambda a: a.astype(np.float64)  # noqa: E731
+    hq, hkv = m["num_q_heads"], m["num_kv_heads"]
+    G = hq // hkv
+    inv = oracle.build_inv_freq(THETA)
+    scale = float(np.array([qk_scale_f16_bits()], np.uint16).view(np.float16)[0])
+
+    def rms(x, w):
+        return x / np.sqrt(np.mean(x * x) + EPS) * f(w)
+
+    h = f(m["embed_tokens"][token])
+    caches = []
+    for L in m["layers"]:
+        qkv = f(L["qkv_proj"]) @ rms(h, L["input_norm"])
+        q = _rope_f64(qkv[:hq * D].reshape(hq, D), L["q_norm"], inv, pos)
+        k = _rope_f64(qkv[hq * D:(hq + hkv) * D].reshape(hkv, D), L["k_norm"], inv, pos)
+        v = qkv[(hq + hkv) * D:].reshape(hkv, D)
+        kc, vc = f(L["k_cache"]), f(L["v_cache"])
+        kc[:, pos], vc[:, pos] = k, v
+        caches.append((kc, vc))
+        o = np.zeros((hq, D))
+        for hd in range(hq):
+            s = kc[hd // G, :pos + 1] @ q[hd] * scale
+            p = np.exp(s - s.max())
+            o[hd] = (p / p.sum()) @ vc[hd // G, :pos + 1]
+        h = h + f(L["o_proj"]) @ o.reshape(-1)
+        gu = f(L["gate_up_proj"]) @ rms(h, L["post_attn_norm"])
+        gt, up = np.split(gu, 2)
+        h = h + f(L["down_proj"]) @ (gt / (1.0 + np.exp(-gt)) * up)
+    return f(m["lm_head"]) @ rms(h, m["final_norm"]), caches
+
+
+def test_qwen3_decode_step_against_float64():
+    """The oracle's token step (its ops composed in the graph's order,
+    src/model.rs:3118-3648) against the float64 formulation: logits within
+    1% of their spread, caches written at `pos` within 1 f16 ulp of the
+    float64 K/V (layer 0) and within the f16 noise of later layers.  A
+    dropped residual add, swapped norms, gate/up swapped or a transposed
+    projection moves the logits by O(their spread)."""
+    m = qwen3_tiny_model(960)
+    pos, token = 20, 123
+    ref_logits, ref_caches = _qwen3_step_f64(m, token, pos)
+    logits, nxt = oracle.qwen3_decode_step(m, token, pos, block_n=32, num_splits=3)
+    spread = ref_logits.std()
+    err = np.abs(logits.astype(np.float64) - ref_logits)
+    assert spread > 1.0 and err.max() < 0.01 * spread, (err.max(), spread)
+    assert nxt == int(np.argmax(logits))
+    for li in range(len(m["layers"])):
+        for c in range(2):
+            got = m["layers"][li][("k_cache", "v_cache")[c]]
+            d = np.abs(got[:, pos].astype(np.float64) - ref_caches[li][c][:, pos])
+            # f16 rounding of qkv before the norm: a few 1e-3 on O(1) rows.
+            assert d.max() < (5e-3 if li == 0 else 2e-2), (li, c, d.max())
+            assert np.array_equal(got[:, :pos], ref_caches[li][c][:, :pos].astype(np.float16))
