@@ -88,6 +88,7 @@ SIGNATURES = {
     "grout_embed_rms_norm_decode": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32,
                                             c_vp]),
     "grout_silu_mul_f16": (c_i32, [c_vp] * 3 + [c_i32, c_vp]),
+    "grout_cast_to_f16": (c_i32, [c_vp, c_i32, c_vp, c_i64, c_vp]),
     "grout_qwen3_workspace_bytes": (c_i64, [ctypes.POINTER(Qwen3Model)]),
     "grout_qwen3_decode_step": (c_i32, [ctypes.POINTER(Qwen3Model), c_vp]),
     "grout_qwen3_runner_create": (

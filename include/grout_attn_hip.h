@@ -369,6 +369,21 @@ int32_t grout_decode_runner_run(grout_decode_runner* runner, uint32_t first_posi
 int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner);
 int32_t grout_decode_runner_destroy(grout_decode_runner* runner);
 
+/* -------------------------------------- checkpoint formats (N4) */
+/* Source element types of grout_cast_to_f16 (safetensors dtypes the
+ * reference's loader accepts, src/loader.rs:109-145). */
+#define GROUT_DTYPE_F16 0
+#define GROUT_DTYPE_BF16 1
+#define GROUT_DTYPE_F32 2
+#define GROUT_DTYPE_F64 3
+
+/* Replaces cast_to_f16 (src/loader.rs:107-145) on the device: dst[i] =
+ * f16(src[i]) for n elements, round to nearest even (F64 via f32, as the
+ * reference).  src and dst 16-byte aligned (dst may be a row range of a
+ * merged matrix: concat_weight_rows_2d, src/model.rs:6021-6070). */
+int32_t grout_cast_to_f16(const void* src, int32_t src_dtype, uint16_t* dst, int64_t n,
+                          grout_stream_t stream);
+
 /* ------------------------------------ Qwen3 decode token step (N1) */
 /* The whole decode graph of DecodeCudaGraphRunner (src/model.rs:3118-3648)
  * on this library's kernels: embedding + input RMSNorm of *token, then per

@@ -66,6 +66,8 @@ def lib():
         L.go_argmax_f16.restype = ctypes.c_uint32
         L.go_argmax_f16.argtypes = [_u16p, _i32]
         L.go_silu_mul.argtypes = [_u16p] * 3 + [_i32]
+        L.go_cast_to_f16.restype = _i32
+        L.go_cast_to_f16.argtypes = [ctypes.c_void_p, _i32, _u16p, ctypes.c_int64]
         _lib = L
     return _lib
 
@@ -268,3 +270,20 @@ def qwen3_decode_step(model: dict, token: int, position: int, block_n: int, num_
     normed, hidden = add_rms_norm(hidden_after_attn, ff_down, model["final_norm"], eps)
     logits = gemv_f16(model["lm_head"], normed)              # :3612-3620
     return logits, argmax_f16(logits)                        # :3622-3640
+
+
+CAST_DTYPES = {"F16": 0, "BF16": 1, "F32": 2, "F64": 3}
+
+
+def cast_to_f16(raw: np.ndarray, dtype: str) -> np.ndarray:
+    """Raw little-endian element bytes of a safetensors tensor -> f16."""
+    if dtype not in CAST_DTYPES:
+        raise ValueError(f"unsupported dtype for fp16 cast: {dtype}")
+    raw = np.ascontiguousarray(raw).view(np.uint8)
+    width = {"F16": 2, "BF16": 2, "F32": 4, "F64": 8}[dtype]
+    n = raw.size // width
+    out = np.zeros(n, dtype=np.float16)
+    st = lib().go_cast_to_f16(raw.ctypes.data_as(ctypes.c_void_p), CAST_DTYPES[dtype], _u16(out), n)
+    if st != 0:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return out

@@ -677,3 +677,25 @@ void go_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int32_
         out[i] = go_f32_to_f16((sig * g) * h2f(up[i]));
     }
 }
+
+/* src/loader.rs:107-145 cast_to_f16: F16 bit copy; BF16 -> f32 (exact) ->
+ * f16::from_f32; F32 -> f16::from_f32; F64 -> `x as f32` -> f16::from_f32.
+ * dtype codes: 0 F16, 1 BF16, 2 F32, 3 F64.  Returns -1 on an unknown dtype. */
+int32_t go_cast_to_f16(const void* src, int32_t dtype, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        switch (dtype) {
+            case 0: out[i] = ((const uint16_t*)src)[i]; break;
+            case 1: {
+                uint32_t bits = (uint32_t)((const uint16_t*)src)[i] << 16;
+                float f;
+                memcpy(&f, &bits, 4);
+                out[i] = go_f32_to_f16(f);
+                break;
+            }
+            case 2: out[i] = go_f32_to_f16(((const float*)src)[i]); break;
+            case 3: out[i] = go_f32_to_f16((float)((const double*)src)[i]); break;
+            default: return -1;
+        }
+    }
+    return 0;
+}

@@ -115,6 +115,9 @@ uint32_t go_argmax_f16(const uint16_t* logits, int32_t n);
 /* src/kernels.rs:271-301 silu_mul_2d_f16. */
 void go_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out, int32_t n);
 
+/* src/loader.rs:107-145 cast_to_f16; dtype 0 F16, 1 BF16, 2 F32, 3 F64. */
+int32_t go_cast_to_f16(const void* src, int32_t dtype, uint16_t* out, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

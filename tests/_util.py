@@ -93,3 +93,73 @@ def qwen3_tiny_model(seed_offset: int, layers: int = 2, hidden: int = 256, hq: i
 
     m["inv_freq"] = oracle.build_inv_freq(THETA)
     return m
+
+
+def write_qwen3_checkpoint(path: str, seed_offset: int, layers: int = 2, hidden: int = 256,
+                           hq: int = 4, hkv: int = 2, inter: int = 512, vocab: int = 1000,
+                           tie: bool = False) -> dict:
+    """A Hugging Face-layout Qwen3 checkpoint in `path`: config.json,
+    model.safetensors.index.json and two shards, matrices stored as BF16, the
+    embedding as F16, norms as F32 and the q/k norms of layer 0 as F64 (every
+    dtype the loader converts).  Returns {name: (dtype, torch tensor)}."""
+    import json
+    import os
+
+    import torch
+    from safetensors.torch import save_file
+
+    g = torch.Generator().manual_seed(SEED_BASE % (1 << 62) + seed_offset)
+
+    def rnd(*shape, scale=1.0):
+        return torch.randn(shape, generator=g) * scale
+
+    tensors = {"model.embed_tokens.weight": rnd(vocab, hidden).half(),
+               "model.norm.weight": (1 + 0.1 * rnd(hidden)).float()}
+    if not tie:
+        tensors["lm_head.weight"] = rnd(vocab, hidden, scale=4 / hidden ** 0.5).bfloat16()
+    for i in range(layers):
+        p = f"model.layers.{i}."
+        nd = torch.float64 if i == 0 else torch.float32
+        tensors.update({
+            p + "input_layernorm.weight": (1 + 0.1 * rnd(hidden)).float(),
+            p + "post_attention_layernorm.weight": (1 + 0.1 * rnd(hidden)).float(),
+            p + "self_attn.q_proj.weight": rnd(hq * D, hidden, scale=hidden ** -0.5).bfloat16(),
+            p + "self_attn.k_proj.weight": rnd(hkv * D, hidden, scale=hidden ** -0.5).bfloat16(),
+            p + "self_attn.v_proj.weight": rnd(hkv * D, hidden, scale=hidden ** -0.5).bfloat16(),
+            p + "self_attn.o_proj.weight": rnd(hidden, hq * D, scale=(hq * D) ** -0.5).bfloat16(),
+            p + "self_attn.q_norm.weight": (1 + 0.1 * rnd(D)).to(nd),
+            p + "self_attn.k_norm.weight": (1 + 0.1 * rnd(D)).to(nd),
+            p + "mlp.gate_proj.weight": rnd(inter, hidden, scale=hidden ** -0.5).bfloat16(),
+            p + "mlp.up_proj.weight": rnd(inter, hidden, scale=hidden ** -0.5).bfloat16(),
+            p + "mlp.down_proj.weight": rnd(hidden, inter, scale=inter ** -0.5).bfloat16(),
+        })
+    names = sorted(tensors)
+    shards = {"model-00001-of-00002.safetensors": names[: len(names) // 2],
+              "model-00002-of-00002.safetensors": names[len(names) // 2:]}
+    weight_map = {}
+    for shard, ns in shards.items():
+        save_file({n: tensors[n].contiguous() for n in ns}, os.path.join(path, shard),
+                  metadata={"format": "pt"})
+        weight_map.update({n: shard for n in ns})
+    with open(os.path.join(path, "model.safetensors.index.json"), "w") as fh:
+        json.dump({"metadata": {"total_size": 0}, "weight_map": weight_map}, fh)
+    cfg = {"architectures": ["Qwen3ForCausalLM"], "vocab_size": vocab, "hidden_size": hidden,
+           "intermediate_size": inter, "num_hidden_layers": layers, "num_attention_heads": hq,
+           "num_key_value_heads": hkv, "head_dim": D, "rms_norm_eps": EPS, "rope_theta": THETA,
+           "max_position_embeddings": 40960, "tie_word_embeddings": tie,
+           "use_sliding_window": False, "eos_token_id": 151645, "torch_dtype": "bfloat16"}
+    with open(os.path.join(path, "config.json"), "w") as fh:
+        json.dump(cfg, fh)
+    st = {torch.float16: "F16", torch.bfloat16: "BF16", torch.float32: "F32",
+          torch.float64: "F64"}
+    return {n: (st[t.dtype], t) for n, t in tensors.items()}
+
+
+def raw_bytes(t) -> np.ndarray:
+    """The little-endian element bytes of a CPU torch tensor, as stored by safetensors."""
+    import torch
+
+    width = t.element_size()
+    return t.contiguous().view(torch.uint8 if width == 1 else
+                               {2: torch.int16, 4: torch.int32, 8: torch.int64}[width]
+                               ).numpy().view(np.uint8).reshape(-1)

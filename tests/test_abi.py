@@ -240,6 +240,17 @@ def test_token_step_op_checks(L):
     assert s(A, A, A, 0, S) == -9
 
 
+def test_cast_checks(L):
+    c = L.grout_cast_to_f16
+    # src, dtype, dst, n, stream
+    assert c(0, 1, A, 8, S) == -1
+    assert c(A, 1, U, 8, S) == -2
+    assert c(A, 4, A, 8, S) == -9
+    assert c(A, -1, A, 8, S) == -9
+    assert c(A, 1, A, -1, S) == -9
+    assert c(A, 1, A, 0, S) == 0        # nothing to convert: no launch
+
+
 def _qwen3_model(**over):
     import ctypes
 
