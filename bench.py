@@ -238,6 +238,21 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
         q_grouped = q_out[:hq].view(hkv, G, D)
         fn = lambda: ga.fmha_decode_gqa_split(q_grouped, kc, vc, att, lse, scale_bits, pos_t)  # noqa
         split_us = 1e3 * time_back_to_back(torch, fn, split_steps, 10, stream=s)
+        # The same fused step cycling through 4 layers' caches (552 MB), so no
+        # launch finds its K/V in the 256 MB last-level cache: the situation of
+        # a real token step, where 63 other layers run between two reads of one
+        # layer's cache.
+        kcs = [kc] + [torch.randn_like(kc) for _ in range(3)]
+        vcs = [vc] + [torch.randn_like(vc) for _ in range(3)]
+        it = [0]
+
+        def cold():
+            it[0] += 1
+            c = it[0] % 4
+            ga.decode_fused(qkv, qw, kw, inv, q_out, kcs[c], vcs[c], att, lse, attn_out,
+                            counters, pos_t, EPS, scale_bits, hq, hkv)
+        cold_us = 1e3 * time_back_to_back(torch, cold, split_steps, 12, stream=s)
+        del kcs, vcs
         mfn = lambda: ga.splitk_reduce_merge(att, lse, attn_out)  # noqa: E731
         # A ~4 us kernel launched back to back through the Python mirror is
         # host-bound; per-launch event pairs bound it from above instead.
@@ -246,7 +261,8 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
     bytes_step = decode_bytes(hq, hkv, ctx + 1)
     return dict(
         hq=hq, hkv=hkv, ctx=ctx, num_splits=ns, replays=replays, step_us=step_us,
-        step_gbs=avg_bytes / (step_us * 1e-6) / 1e9, fused_us=fused_us,
+        step_gbs=avg_bytes / (step_us * 1e-6) / 1e9, fused_us=fused_us, cold_us=cold_us,
+        cold_gbs=bytes_step / (cold_us * 1e-6) / 1e9,
         fused_gbs=bytes_step / (fused_us * 1e-6) / 1e9, split_us=split_us, merge_us=merge_us,
         split_gbs=bytes_step / (split_us * 1e-6) / 1e9, bytes_step=bytes_step,
         kc=kc, vc=vc, q=q_out[:hq].clone())
@@ -305,6 +321,67 @@ def bench_decode_layer(torch, ga, steps, gen):
         torch, lambda: L.grout_argmax_f16(*aargs), max(steps, 200), 20))
     assert int(tok.item()) == int(torch.argmax(lg.float()).item()), "argmax mismatch"
     return res
+
+
+def bench_token_step(torch, ga, gen, layers=64, ctx=32768, steps=20):
+    """The whole Qwen3-32B decode token step (hidden 5120, 64 Q / 8 KV heads,
+    intermediate 25600, vocab 151936, `layers` layers) as one hipGraph, every
+    layer's KV cache holding `ctx` tokens: `steps` replays issued back to back
+    from C, each embedding the token the previous one picked.  Random f16
+    weights; bytes per token = every weight matrix + the KV read and written."""
+    hidden, inter, vocab, hq, hkv = 5120, 25600, 151936, 64, 8
+    MS = ctx + 1024
+    dev = "cuda"
+
+    def mat(m, k, scale=1.0):
+        return torch.empty((m, k), dtype=torch.float16, device=dev).normal_(
+            0.0, scale / math.sqrt(k), generator=gen)
+
+    def nw(n):
+        return torch.empty((n,), dtype=torch.float16, device=dev).normal_(1.0, 0.1, generator=gen)
+
+    def cache():
+        return torch.empty((hkv, MS, D), dtype=torch.float16, device=dev).normal_(generator=gen)
+
+    lay = [dict(input_norm=nw(hidden), qkv_proj=mat((hq + 2 * hkv) * D, hidden), q_norm=nw(D),
+                k_norm=nw(D), o_proj=mat(hidden, hq * D), post_attn_norm=nw(hidden),
+                gate_up_proj=mat(2 * inter, hidden), down_proj=mat(hidden, inter),
+                k_cache=cache(), v_cache=cache()) for _ in range(layers)]
+    embed = torch.empty((vocab, hidden), dtype=torch.float16, device=dev).normal_(generator=gen)
+    lm_head = mat(vocab, hidden, 4.0)
+    token = torch.tensor([1], dtype=torch.int32, device=dev)
+    position = torch.zeros((1,), dtype=torch.int32, device=dev)
+    logits = torch.empty((vocab,), dtype=torch.float16, device=dev)
+    scale_bits = int(torch.tensor([1.0 / math.sqrt(D)], dtype=torch.float16).view(torch.int16)
+                     .item()) & 0xFFFF
+    runner = ga.Qwen3DecodeRunner(
+        layers=lay, embed_tokens=embed, final_norm=nw(hidden), lm_head=lm_head,
+        inv_freq=ga.build_inv_freq(THETA).cuda(), token=token, position=position, logits=logits,
+        num_q_heads=hq, num_kv_heads=hkv, eps=EPS, qk_scale_f16_bits=scale_bits,
+        prime_position=ctx)
+    s = runner.stream
+    try:
+        runner.run(ctx + 1, 3)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        runner.run(ctx + 4, steps)
+        b.record(s)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / steps
+        assert torch.isfinite(logits).all().item(), "non-finite logits"
+        assert int(position.item()) == ctx + 4 + steps
+    finally:
+        runner.close()
+    w_layer = 2 * hidden * ((hq + 2 * hkv) * D + hq * D + 3 * inter)
+    avg_ctx = ctx + 4 + (steps + 1) / 2
+    kv_layer = 2 * hkv * avg_ctx * D * 2 + 2 * hkv * D * 2
+    nbytes = layers * (w_layer + kv_layer) + 2 * vocab * hidden + 2 * hidden
+    del lay, embed, lm_head
+    torch.cuda.empty_cache()
+    return dict(ms=ms, tokens_per_s=1e3 / ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9,
+                layers=layers, ctx=ctx, steps=steps, num_splits=runner.num_splits)
 
 
 def bench_mfma_probe(torch, launches: int = 8):
@@ -391,7 +468,7 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "prefill", "prefill-split", "decode", "norm", "kv",
-                                       "mfma-probe", "decode-layer"],
+                                       "mfma-probe", "decode-layer", "token-step"],
                     default="all",
                     help="run one workload only (for profiling runs); prints no JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -448,6 +525,10 @@ def main(argv=None) -> int:
             log("decode layer c4: " + ", ".join(
                 f"{k} {v['us']:.2f} us" + (f" ({v['gbs']:.0f} GB/s)" if "gbs" in v else "")
                 for k, v in dl.items()))
+        elif args.only == "token-step":
+            ts = bench_token_step(torch, ga, gen, steps=args.steps)
+            log(f"token step c4 ({ts['layers']} layers, ctx {ts['ctx']}): {ts['ms']:.3f} ms/token, "
+                f"{ts['tokens_per_s']:.1f} tok/s, {ts['gbs']:.0f} GB/s")
         elif args.only == "mfma-probe":
             mp = bench_mfma_probe(torch)
             log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
@@ -478,7 +559,8 @@ def main(argv=None) -> int:
     log("decode c4 ...")
     dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, 20, gen, 200)
     log(f"decode c4: graph step {dec['step_us']:.2f} us ({dec['step_gbs']:.0f} GB/s), "
-        f"fused kernel {dec['fused_us']:.2f} us ({dec['fused_gbs']:.0f} GB/s), "
+        f"fused kernel {dec['fused_us']:.2f} us ({dec['fused_gbs']:.0f} GB/s; "
+        f"caches cycled {dec['cold_us']:.2f} us, {dec['cold_gbs']:.0f} GB/s), "
         f"split {dec['split_us']:.2f} us ({dec['split_gbs']:.0f} GB/s), "
         f"merge {dec['merge_us']:.2f} us, NKS={dec['num_splits']}")
     log("decode layer ops c4 ...")
@@ -486,6 +568,10 @@ def main(argv=None) -> int:
     log("decode layer c4: " + ", ".join(
         f"{k} {v['us']:.2f} us" + (f" ({v['gbs']:.0f} GB/s)" if "gbs" in v else "")
         for k, v in dl.items()))
+    log("token step c4 ...")
+    ts = bench_token_step(torch, ga, gen)
+    log(f"token step c4 ({ts['layers']} layers, ctx {ts['ctx']}): {ts['ms']:.3f} ms/token, "
+        f"{ts['tokens_per_s']:.1f} tok/s, {ts['gbs']:.0f} GB/s")
     log("decode c2 ...")
     dec2 = bench_decode(torch, ga, 32, 8, 4096, 200, 20, gen, 200)
     log(f"decode c2: graph step {dec2['step_us']:.2f} us, fused {dec2['fused_us']:.2f} us, "
@@ -538,6 +624,8 @@ def main(argv=None) -> int:
             "value": round(dec["step_gbs"], 1), "unit": "GB/s",
             "us_per_step": round(dec["step_us"], 3), "num_splits": dec["num_splits"],
             "fused_kernel_us": round(dec["fused_us"], 3),
+            "fused_kernel_cold_cache_us": round(dec["cold_us"], 3),
+            "fused_kernel_cold_cache_gbs": round(dec["cold_gbs"], 1),
             "standalone_split_us": round(dec["split_us"], 3),
             "standalone_merge_us": round(dec["merge_us"], 3),
             "roofline": rl("hbm", dec["fused_gbs"], PEAK_HBM_GBS, "GB/s",
@@ -562,6 +650,14 @@ def main(argv=None) -> int:
                for nm in ("qkv_proj", "o_proj", "lm_head")},
             "add_rms_norm_us": round(dl["add_rms_norm"]["us"], 2),
             "argmax_us": round(dl["argmax"]["us"], 2)},
+        "token_step_c4": {
+            "workload": f"Qwen3-32B-shaped decode token step, {ts['layers']} layers, every KV "
+                        f"cache at context {ts['ctx']}, one hipGraph per token (embedding .. "
+                        "argmax), random f16 weights",
+            "ms_per_token": round(ts["ms"], 3), "tokens_per_s": round(ts["tokens_per_s"], 2),
+            "bytes_per_token": ts["bytes"], "GB/s": round(ts["gbs"], 1),
+            "frac_of_hbm_peak": round(ts["gbs"] / PEAK_HBM_GBS, 4),
+            "num_splits": ts["num_splits"], "steps": ts["steps"]},
         "qk_norm_rope_c3": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                             "frac_of_hbm_peak": round(nrm["gbs"] / PEAK_HBM_GBS, 4)},
         "kv_cache_update_c3": {"us": round(kvu["ms"] * 1e3, 2), "GB/s": round(kvu["gbs"], 1),
