@@ -93,8 +93,11 @@ class SafetensorsFile:
 
     def __init__(self, path: str):
         self.path = path
-        with open(path, "rb") as fh:
-            self._mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+        try:
+            with open(path, "rb") as fh:
+                self._mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+        except (OSError, ValueError) as e:  # missing, unreadable or empty file
+            raise GroutError(f"failed to map {path}: {e}") from e
         size = len(self._mm)
         _ensure(size >= 8, f"{path}: not a safetensors file")
         (n,) = struct.unpack("<Q", self._mm[:8])
@@ -103,12 +106,16 @@ class SafetensorsFile:
             header = json.loads(bytes(self._mm[8:8 + n]))
         except (json.JSONDecodeError, UnicodeDecodeError) as e:
             raise GroutError(f"{path}: bad header: {e}") from e
+        _ensure(isinstance(header, dict), f"{path}: bad header: not a JSON object")
         self.data_start = 8 + n
         self.metadata = header.pop("__metadata__", None)
         self.tensors = {}
         for name, info in header.items():
-            dtype, shape = info["dtype"], [int(x) for x in info["shape"]]
-            b, e = (int(x) for x in info["data_offsets"])
+            try:
+                dtype, shape = info["dtype"], [int(x) for x in info["shape"]]
+                b, e = (int(x) for x in info["data_offsets"])
+            except (KeyError, TypeError, ValueError) as err:
+                raise GroutError(f"{path}: bad header entry `{name}`: {err!r}") from err
             count = 1
             for s in shape:
                 count *= s

@@ -340,7 +340,7 @@ extern "C" int32_t grout_silu_mul_f16(const uint16_t* gate, const uint16_t* up, 
     GROUT_REQUIRE_PTR(gate);
     GROUT_REQUIRE_PTR(up);
     GROUT_REQUIRE_PTR(out);
-    GROUT_REQUIRE(n >= 8 && n % 8 == 0, GROUT_ERR_ARG);
+    GROUT_REQUIRE(n >= 8 && n % 8 == 0 && n <= (1 << 30), GROUT_ERR_ARG);
     const unsigned blocks = static_cast<unsigned>((n / 8 + kPointwiseThreads - 1) / kPointwiseThreads);
     hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(kPointwiseThreads), 0, to_hip(stream),
                        gate, up, out, n);
@@ -369,8 +369,11 @@ extern "C" int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uin
     return launch_status();
 }
 
+// Logit counts up to 2^30 (block offsets stay inside int).
+constexpr int32_t kArgmaxMaxN = 1 << 30;
+
 extern "C" int32_t grout_argmax_blocks(int32_t n) {
-    if (n < 1) return GROUT_ERR_ARG;
+    if (n < 1 || n > kArgmaxMaxN) return GROUT_ERR_ARG;
     return (n + kArgmaxBlock - 1) / kArgmaxBlock;
 }
 
@@ -382,7 +385,7 @@ extern "C" int32_t grout_argmax_f16(const uint16_t* logits, float* block_max, ui
     GROUT_REQUIRE(((reinterpret_cast<uintptr_t>(block_max) | reinterpret_cast<uintptr_t>(block_idx) |
                     reinterpret_cast<uintptr_t>(token)) & 3u) == 0,
                   GROUT_ERR_ALIGNMENT);
-    GROUT_REQUIRE(n >= 1, GROUT_ERR_ARG);
+    GROUT_REQUIRE(n >= 1 && n <= kArgmaxMaxN, GROUT_ERR_ARG);
     const int nblocks = (n + kArgmaxBlock - 1) / kArgmaxBlock;
     hipLaunchKernelGGL(argmax_blocks_kernel, dim3(nblocks), dim3(kArgmaxThreads), 0, to_hip(stream),
                        logits, n, block_max, block_idx);

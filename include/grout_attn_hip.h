@@ -209,7 +209,8 @@ int32_t grout_embed_rms_norm_decode(const uint32_t* token, const uint16_t* table
 
 /* Replaces silu_mul_2d_f16 (src/kernels.rs:271-301; src/model.rs:3556-3565):
  * out[i] = f16(sigmoid(g) * g * u), g = f32(gate[i]), u = f32(up[i]),
- * sigmoid(g) = 1 / (1 + exp(-g)).  n a multiple of 8; 16-byte aligned. */
+ * sigmoid(g) = 1 / (1 + exp(-g)).  n a multiple of 8, at most 2^30; 16-byte
+ * aligned. */
 int32_t grout_silu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int32_t n,
                            grout_stream_t stream);
 
@@ -223,7 +224,8 @@ int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uint16_t* out,
 /* Replaces argmax_blocks_f16 + argmax_reduce_blocks_to_u32 (src/kernels.rs:345-392,
  * 458-505), the in-graph greedy token pick: *token = the lowest index of the
  * largest f32(logits[i]) over [0, n) (NaN logits are never picked).
- * block_max / block_idx: grout_argmax_blocks(n) entries of scratch each. */
+ * block_max / block_idx: grout_argmax_blocks(n) entries of scratch each.
+ * 1 <= n <= 2^30. */
 int32_t grout_argmax_blocks(int32_t n);
 int32_t grout_argmax_f16(const uint16_t* logits, float* block_max, uint32_t* block_idx,
                          uint32_t* token, int32_t n, grout_stream_t stream);
@@ -456,6 +458,8 @@ int32_t grout_qwen3_runner_step(grout_qwen3_runner* runner, uint32_t position,
 int32_t grout_qwen3_runner_run(grout_qwen3_runner* runner, uint32_t first_position,
                                int32_t count);
 int32_t grout_qwen3_runner_destroy(grout_qwen3_runner* runner);
+/* A runner is used from one host thread at a time; two runners sharing a
+ * workspace, token or position buffer race on the device. */
 
 #ifdef __cplusplus
 }

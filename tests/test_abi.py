@@ -215,6 +215,7 @@ def test_decode_layer_checks(L):
     assert g(A, A, A, 8, 12, S) == -9
     assert g(A, A, A, 8, 32776, S) == -9
     assert L.grout_argmax_blocks(0) == -9
+    assert L.grout_argmax_blocks((1 << 30) + 1) == -9
     assert [L.grout_argmax_blocks(n) for n in (1, 2048, 2049, 151936)] == [1, 1, 2, 75]
     a = L.grout_argmax_f16
     # logits, block_max, block_idx, token, n, stream

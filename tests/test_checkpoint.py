@@ -86,6 +86,15 @@ def test_loader_errors(ckpt, tmp_path):
     bad.write_bytes(len(hdr).to_bytes(8, "little") + hdr + bytes(8))
     with pytest.raises(grout_amd.GroutError, match="do not match"):
         SafetensorsFile(str(bad))
+    odd = tmp_path / "odd.safetensors"
+    hdr = json.dumps({"x": {"dtype": "BF16", "shape": [4]}}).encode()   # no data_offsets
+    odd.write_bytes(len(hdr).to_bytes(8, "little") + hdr + bytes(8))
+    with pytest.raises(grout_amd.GroutError, match="bad header entry"):
+        SafetensorsFile(str(odd))
+    empty = tmp_path / "empty.safetensors"
+    empty.write_bytes(b"")
+    with pytest.raises(grout_amd.GroutError, match="failed to map"):
+        SafetensorsFile(str(empty))
     trunc = tmp_path / "trunc.safetensors"
     trunc.write_bytes((1 << 40).to_bytes(8, "little") + b"{}")
     with pytest.raises(grout_amd.GroutError, match="past the end"):
