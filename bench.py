@@ -421,6 +421,38 @@ def bench_mfma_probe(torch, launches: int = 8):
     return dict(qk=res[0], pv=res[1], mix=mix, blocks=blocks)
 
 
+def bench_hbm_probe(torch, gib: int = 4, launches: int = 5):
+    """Sustained HBM read rate of a plain streaming kernel (grout_amd/probe/hbm_read.hip)
+    over a buffer far larger than the 256 MB last-level cache: the practical ceiling of the
+    HBM-bound kernels.  GB/s (1e9 bytes)."""
+    import ctypes
+
+    from grout_amd import build as gbuild
+
+    lib = ctypes.CDLL(gbuild.PROBE_LIB_PATH)
+    fn = lib.grout_probe_hbm_read
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
+    nbytes = gib << 30
+    src = torch.empty((nbytes,), dtype=torch.uint8, device="cuda").fill_(1)
+    blocks = 8 * torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty((blocks * 256,), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    for _ in range(2):
+        assert fn(src.data_ptr(), nbytes, out.data_ptr(), blocks, stream.cuda_stream) == 0
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(launches):
+        assert fn(src.data_ptr(), nbytes, out.data_ptr(), blocks, stream.cuda_stream) == 0
+    b.record(stream)
+    torch.cuda.synchronize()
+    gbs = launches * nbytes / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src
+    torch.cuda.empty_cache()
+    return dict(gbs=gbs, bytes=nbytes, blocks=blocks)
+
+
 def cpu_baseline_prefill(torch, pre, threads: int):
     """Oracle fp32 attention over every query row of the c3 inputs (about 10 s on 16 cores)."""
     import oracle
@@ -468,7 +500,7 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "prefill", "prefill-split", "decode", "norm", "kv",
-                                       "mfma-probe", "decode-layer", "token-step"],
+                                       "mfma-probe", "decode-layer", "token-step", "hbm-probe"],
                     default="all",
                     help="run one workload only (for profiling runs); prints no JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -529,6 +561,9 @@ def main(argv=None) -> int:
             ts = bench_token_step(torch, ga, gen, steps=args.steps)
             log(f"token step c4 ({ts['layers']} layers, ctx {ts['ctx']}): {ts['ms']:.3f} ms/token, "
                 f"{ts['tokens_per_s']:.1f} tok/s, {ts['gbs']:.0f} GB/s")
+        elif args.only == "hbm-probe":
+            hp = bench_hbm_probe(torch)
+            log(f"hbm read probe: {hp['gbs']:.0f} GB/s over {hp['bytes'] >> 30} GiB")
         elif args.only == "mfma-probe":
             mp = bench_mfma_probe(torch)
             log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
@@ -551,6 +586,8 @@ def main(argv=None) -> int:
     mp = bench_mfma_probe(torch)
     log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
         f"mix {mp['mix']:.0f} TFLOP/s; prefill = {pre['tflops'] / mp['mix']:.3f} of the mix")
+    hp = bench_hbm_probe(torch)
+    log(f"hbm read probe: {hp['gbs']:.0f} GB/s over {hp['bytes'] >> 30} GiB")
     log("qk_norm_rope c3 ...")
     nrm = bench_norm(torch, ga, args.steps, args.warmup, gen)
     log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
@@ -617,6 +654,10 @@ def main(argv=None) -> int:
             "mix": round(mp["mix"], 1), "frac_of_nominal_peak": round(mp["mix"] / PEAK_TFLOPS_F16, 4),
             "prefill_frac_of_mix": round(pre["tflops"] / mp["mix"], 4),
             "source": "grout_amd/probe/mfma_ceiling.hip"},
+        # What a plain streaming read kernel sustains on this GPU (cache-cold, 4 GiB).
+        "hbm_read_probe": {"unit": "GB/s", "value": round(hp["gbs"], 1),
+                           "frac_of_peak": round(hp["gbs"] / PEAK_HBM_GBS, 4),
+                           "source": "grout_amd/probe/hbm_read.hip"},
         "decode": {
             "workload": "c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context 32768, "
                         f"hipGraph x{dec['replays']} of the fused step (norm/RoPE/KV write + "
@@ -631,6 +672,7 @@ def main(argv=None) -> int:
             "roofline": rl("hbm", dec["fused_gbs"], PEAK_HBM_GBS, "GB/s",
                            traffic=round(PMC_TRAFFIC_BYTES["attn_decode_fused_c4"])),
             "step_frac_of_hbm_peak": round(dec["step_gbs"] / PEAK_HBM_GBS, 4),
+            "fused_kernel_frac_of_read_probe": round(dec["fused_gbs"] / hp["gbs"], 4),
             "hip_graph_packet_capture": GRAPH_PACKET_CAPTURE,
             "cpu_baseline": cpu_dec,
         },

@@ -177,3 +177,38 @@ def test_token_step_single_layer_gqa8(gpu):
         _check_caches(dm, ref, [100, 101])
     finally:
         runner.close()
+
+
+def test_token_step_qwen3_06b_shapes(gpu):
+    """Two layers at Qwen3-0.6B shapes (config c1's model: hidden 1024, 16 Q / 8 KV heads,
+    intermediate 3072) with the full 151936-token vocabulary: lm_head GEMV and argmax at
+    their real sizes inside the graph."""
+    import torch
+    import grout_amd
+
+    m = qwen3_tiny_model(1650, layers=2, hidden=1024, hq=16, hkv=8, inter=3072, vocab=151936,
+                         max_seq=64, filled=30)
+    ref = copy.deepcopy(m)
+    dm = _device_model(torch, m)
+    token = torch.tensor([151000], dtype=torch.int32, device="cuda")
+    position = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    logits = torch.zeros((151936,), dtype=torch.float16, device="cuda")
+    print("[qwen3 step] Qwen3-0.6B shapes, vocab 151936", flush=True)
+    runner = grout_amd.Qwen3DecodeRunner(
+        **dm, token=token, position=position, logits=logits, num_q_heads=16, num_kv_heads=8,
+        eps=m["eps"], qk_scale_f16_bits=m["qk_scale_f16_bits"], num_splits=2, block_n=32,
+        prime_position=30)
+    try:
+        torch.cuda.synchronize()
+        tok = 151000
+        for pos in (30, 31, 32):
+            if pos > 30:
+                runner.step(pos)
+            rl, _ = oracle.qwen3_decode_step(ref, tok, pos, 32, 2)
+            gl = logits.cpu().numpy()
+            assert_close_attn(gl, rl, f"position {pos} logits", atol=1e-2, rtol=1e-2)
+            tok = int(token.item())
+            assert tok == oracle.argmax_f16(gl)
+        _check_caches(dm, ref, [30, 31, 32])
+    finally:
+        runner.close()
