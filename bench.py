@@ -252,6 +252,12 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
             ga.decode_fused(qkv, qw, kw, inv, q_out, kcs[c], vcs[c], att, lse, attn_out,
                             counters, pos_t, EPS, scale_bits, hq, hkv)
         cold_us = 1e3 * time_back_to_back(torch, cold, split_steps, 12, stream=s)
+
+        def split_cold():
+            it[0] += 1
+            c = it[0] % 4
+            ga.fmha_decode_gqa_split(q_grouped, kcs[c], vcs[c], att, lse, scale_bits, pos_t)
+        split_cold_us = 1e3 * time_back_to_back(torch, split_cold, split_steps, 12, stream=s)
         del kcs, vcs
         mfn = lambda: ga.splitk_reduce_merge(att, lse, attn_out)  # noqa: E731
         # A ~4 us kernel launched back to back through the Python mirror is
@@ -262,6 +268,7 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
     return dict(
         hq=hq, hkv=hkv, ctx=ctx, num_splits=ns, replays=replays, step_us=step_us,
         step_gbs=avg_bytes / (step_us * 1e-6) / 1e9, fused_us=fused_us, cold_us=cold_us,
+        split_cold_us=split_cold_us,
         cold_gbs=bytes_step / (cold_us * 1e-6) / 1e9,
         fused_gbs=bytes_step / (fused_us * 1e-6) / 1e9, split_us=split_us, merge_us=merge_us,
         split_gbs=bytes_step / (split_us * 1e-6) / 1e9, bytes_step=bytes_step,
@@ -572,7 +579,8 @@ def main(argv=None) -> int:
             dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, args.warmup, gen,
                                args.steps)
             log(f"decode c4: graph step {dec['step_us']:.2f} us, fused {dec['fused_us']:.2f} us "
-                f"({dec['fused_gbs']:.0f} GB/s), split {dec['split_us']:.2f} us")
+                f"({dec['fused_gbs']:.0f} GB/s; caches cycled {dec['cold_us']:.2f} us), split "
+                f"{dec['split_us']:.2f} us (caches cycled {dec['split_cold_us']:.2f} us)")
         return 0
 
     log("prefill c3 ...")
@@ -598,7 +606,8 @@ def main(argv=None) -> int:
     log(f"decode c4: graph step {dec['step_us']:.2f} us ({dec['step_gbs']:.0f} GB/s), "
         f"fused kernel {dec['fused_us']:.2f} us ({dec['fused_gbs']:.0f} GB/s; "
         f"caches cycled {dec['cold_us']:.2f} us, {dec['cold_gbs']:.0f} GB/s), "
-        f"split {dec['split_us']:.2f} us ({dec['split_gbs']:.0f} GB/s), "
+        f"split {dec['split_us']:.2f} us ({dec['split_gbs']:.0f} GB/s; caches cycled "
+        f"{dec['split_cold_us']:.2f} us), "
         f"merge {dec['merge_us']:.2f} us, NKS={dec['num_splits']}")
     log("decode layer ops c4 ...")
     dl = bench_decode_layer(torch, ga, args.steps, gen)
@@ -668,6 +677,9 @@ def main(argv=None) -> int:
             "fused_kernel_cold_cache_us": round(dec["cold_us"], 3),
             "fused_kernel_cold_cache_gbs": round(dec["cold_gbs"], 1),
             "standalone_split_us": round(dec["split_us"], 3),
+            "standalone_split_cold_cache_us": round(dec["split_cold_us"], 3),
+            "standalone_split_cold_cache_frac_of_hbm_peak": round(
+                dec["bytes_step"] / (dec["split_cold_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "standalone_merge_us": round(dec["merge_us"], 3),
             "roofline": rl("hbm", dec["fused_gbs"], PEAK_HBM_GBS, "GB/s",
                            traffic=round(PMC_TRAFFIC_BYTES["attn_decode_fused_c4"])),
