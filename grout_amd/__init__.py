@@ -384,15 +384,26 @@ class Qwen3DecodeRunner:
                   "post_attn_norm": (hidden,), "gate_up_proj": (2 * inter, hidden),
                   "down_proj": (hidden, inter), "k_cache": (hkv, max_seq, d),
                   "v_cache": (hkv, max_seq, d)}
+        # Shapes first (the reference's ensure! order), then dtypes and devices.
         for i, L in enumerate(layers):
             for key in QWEN3_LAYER_KEYS:
                 _ensure(key in L, f"layer {i} has no {key}")
                 _ensure(tuple(L[key].shape) == shapes[key],
                         f"layer {i} {key} shape {list(L[key].shape)} != {list(shapes[key])}")
-                _f16(L[key], f"layer {i} {key}")
         _ensure(tuple(lm_head.shape) == (vocab, hidden), "lm_head must be [vocab, hidden]")
         _ensure(final_norm.numel() == hidden and logits.numel() == vocab,
                 "final_norm [hidden] and logits [vocab] expected")
+        for i, L in enumerate(layers):
+            for key in QWEN3_LAYER_KEYS:
+                _f16(L[key], f"layer {i} {key}")
+        for t, nm in ((embed_tokens, "embed_tokens"), (lm_head, "lm_head"),
+                      (final_norm, "final_norm"), (logits, "logits")):
+            _f16(t, nm)
+        _ensure(inv_freq.dtype == torch.float32 and inv_freq.is_cuda and inv_freq.numel() == 64,
+                "inv_freq must be a device float32 [64] tensor (build_inv_freq)")
+        for t, nm in ((token, "token"), (position, "position")):
+            _ensure(t.dtype in (torch.int32, torch.uint32) and t.is_cuda and t.numel() >= 1,
+                    f"{nm} must be a device int32 tensor")
         if num_splits is None:
             num_splits = pick_num_splits(max_seq, hkv, block_n)
         self._layers = (_lib.Qwen3Layer * len(layers))(*[

@@ -367,6 +367,24 @@ def test_python_mirror_shape_errors():
         grout_amd.gemv_f16(wm, torch.zeros(32, dtype=h), torch.zeros(16, dtype=h))
     with pytest.raises(grout_amd.GroutError, match="out must have 16 elements"):
         grout_amd.gemv_f16(wm, torch.zeros(64, dtype=h), torch.zeros(15, dtype=h))
+    lay = {"input_norm": torch.zeros(256, dtype=h), "qkv_proj": torch.zeros((1024, 256), dtype=h),
+           "q_norm": torch.zeros(128, dtype=h), "k_norm": torch.zeros(128, dtype=h),
+           "o_proj": torch.zeros((256, 512), dtype=h), "post_attn_norm": torch.zeros(256, dtype=h),
+           "gate_up_proj": torch.zeros((1024, 256), dtype=h),
+           "down_proj": torch.zeros((256, 512), dtype=h),
+           "k_cache": torch.zeros((2, 16, 128), dtype=h), "v_cache": torch.zeros((2, 16, 128), dtype=h)}
+    kw = dict(embed_tokens=torch.zeros((10, 256), dtype=h), final_norm=torch.zeros(256, dtype=h),
+              lm_head=torch.zeros((10, 256), dtype=h), inv_freq=torch.zeros(64),
+              token=torch.zeros(1, dtype=torch.int32), position=torch.zeros(1, dtype=torch.int32),
+              logits=torch.zeros(10, dtype=h), num_q_heads=4, num_kv_heads=2, eps=1e-6,
+              qk_scale_f16_bits=0x2DA8)
+    with pytest.raises(grout_amd.GroutError, match="o_proj shape"):
+        grout_amd.Qwen3DecodeRunner(layers=[dict(lay, o_proj=torch.zeros((256, 256), dtype=h))],
+                                    **kw)
+    with pytest.raises(grout_amd.GroutError, match="lm_head must be"):
+        grout_amd.Qwen3DecodeRunner(layers=[lay], **dict(kw, lm_head=torch.zeros((9, 256), dtype=h)))
+    with pytest.raises(grout_amd.GroutError, match="must be a device tensor"):
+        grout_amd.Qwen3DecodeRunner(layers=[lay], **kw)   # CPU tensors
     with pytest.raises(grout_amd.GroutError, match="weight must have 64 elements"):
         z = torch.zeros(64, dtype=h)
         grout_amd.add_rms_norm_decode(z, z, torch.zeros(32, dtype=h), z, z, 1e-6)
