@@ -392,10 +392,11 @@ def bench_token_step(torch, ga, gen, layers=64, ctx=32768, steps=20):
 
 
 def bench_mfma_probe(torch, launches: int = 8):
-    """Sustained v_mfma_f32_32x32x16_f16 rate for operands distributed like the
-    prefill kernel's (grout_amd/probe/mfma_ceiling.hip): mode 0 = both N(0,1)
-    (Q K^T), mode 1 = N(0,1) x [0,1) (P V).  Returns TFLOP/s per mode and the
-    rate of an equal mix of the two (harmonic mean: equal MFMA counts)."""
+    """Sustained v_mfma_f32_32x32x16_f16 rate for operand data distributed like the
+    prefill kernel's (grout_amd/probe/mfma_ceiling.hip), operands loaded once from
+    16 MB f16 buffers: A ~ N(0,1) with B ~ N(0,1) (the Q K^T kind) or B = u1*u2 in
+    [0,1) (the P V kind).  Returns TFLOP/s per kind and the rate of an equal mix of
+    the two (harmonic mean: equal MFMA counts)."""
     import ctypes
 
     from grout_amd import build as gbuild
@@ -405,27 +406,37 @@ def bench_mfma_probe(torch, launches: int = 8):
     lib = ctypes.CDLL(gbuild.PROBE_LIB_PATH)
     fn = lib.grout_probe_mfma_f16
     fn.restype = ctypes.c_int32
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
-                   ctypes.c_void_p]
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32,
+                   ctypes.c_int32, ctypes.c_void_p]
     blocks = torch.cuda.get_device_properties(0).multi_processor_count
     iters = 4000
+    n_chunks = 1 << 20
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x67726F7574000009)
+    a_ops = torch.randn((n_chunks * 8,), device="cuda", generator=gen).half()
+    b_kinds = {"qk": torch.randn((n_chunks * 8,), device="cuda", generator=gen).half(),
+               "pv": (torch.rand((n_chunks * 8,), device="cuda", generator=gen) *
+                      torch.rand((n_chunks * 8,), device="cuda", generator=gen)).half()}
     out = torch.empty((blocks * 512,), device="cuda", dtype=torch.float32)
     stream = torch.cuda.current_stream()
     res = {}
-    for mode in (0, 1):
-        for i in range(3):
-            assert fn(out.data_ptr(), blocks, iters, mode, i, stream.cuda_stream) == 0
+    for kind, b_ops in b_kinds.items():
+        call = lambda: fn(a_ops.data_ptr(), b_ops.data_ptr(), n_chunks, out.data_ptr(), blocks, iters,
+                          stream.cuda_stream)
+        for _ in range(3):
+            assert call() == 0
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        for i in range(launches):
-            assert fn(out.data_ptr(), blocks, iters, mode, 100 + i, stream.cuda_stream) == 0
+        for _ in range(launches):
+            assert call() == 0
         b.record(stream)
         torch.cuda.synchronize()
         flops = launches * blocks * 8.0 * iters * 16 * 32768
-        res[mode] = flops / (a.elapsed_time(b) * 1e-3) / 1e12
-    mix = 2.0 / (1.0 / res[0] + 1.0 / res[1])
-    return dict(qk=res[0], pv=res[1], mix=mix, blocks=blocks)
+        res[kind] = flops / (a.elapsed_time(b) * 1e-3) / 1e12
+    mix = 2.0 / (1.0 / res["qk"] + 1.0 / res["pv"])
+    del a_ops, b_kinds
+    return dict(qk=res["qk"], pv=res["pv"], mix=mix, blocks=blocks)
 
 
 def bench_hbm_probe(torch, gib: int = 4, launches: int = 5):
