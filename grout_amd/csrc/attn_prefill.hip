@@ -317,6 +317,10 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
 #pragma unroll
             for (int r = 0; r < 16; ++r) s[mb][r] = 0.0f;
         half8_t ring[kRing];
+        // Issue priority above the softmax-phase wave on the same SIMD while
+        // feeding the matrix core (measured: ~1% faster; raising the softmax
+        // phase instead does nothing).
+        __builtin_amdgcn_s_setprio(2);
 #pragma unroll
         for (int i = 0; i < kPfAhead; ++i) ring[i % kRing] = read_op(i);
 #pragma unroll
@@ -329,6 +333,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     // Softmax phase of tile j: mask, running max (lazy), P = 2^(c*s - m), row sum.
