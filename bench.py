@@ -96,6 +96,28 @@ def time_launches(torch, fn, steps: int, warmup: int, stream=None):
     return durs, wall
 
 
+def time_region(torch, fn, steps: int, warmup: int, stream=None):
+    """The timed region of the bench contract: `warmup` untimed launches, a
+    synchronization, then exactly `steps` launches back to back between two
+    events on the launch stream and a synchronization.  Returns the average
+    duration per launch (ms, from the events) and the host wall time of the
+    region (ms)."""
+    s = stream or torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record(s)
+    for _ in range(steps):
+        fn()
+    b.record(s)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    return a.elapsed_time(b) / steps, wall
+
+
 def time_back_to_back(torch, fn, n: int, warmup: int, stream=None) -> float:
     """Average duration (ms) of n launches issued back to back between two events."""
     s = stream or torch.cuda.current_stream()
@@ -119,9 +141,8 @@ def bench_prefill(torch, ga, steps, warmup, gen):
     vc = torch.randn((hkv, S, D), device="cuda", generator=gen, dtype=torch.float32).half()
     out = torch.empty_like(q)
     fn = lambda: ga.attend_prefill(q, kc, vc, out, 0)  # noqa: E731
-    durs, wall = time_launches(torch, fn, steps, warmup)
+    ms, wall = time_region(torch, fn, steps, warmup)
     assert torch.isfinite(out).all().item(), "non-finite prefill output"
-    ms = sum(durs) / len(durs)
     flops = prefill_flops(hq, S)
     tflops = flops / (ms * 1e-3) / 1e12
     return dict(q=q, kc=kc, vc=vc, out=out, ms=ms, wall_ms=wall, tflops=tflops, flops=flops,
