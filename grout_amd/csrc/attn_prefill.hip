@@ -449,6 +449,9 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     const int row = row0 + l32;
     const float lt = l_run + swap_halves(l_run);
     const float l_safe = fmaxf(lt, 1.0e-8f);
+    // O / l_safe is a true division per element, the reference's true_div
+    // (src/kernels.rs:1289-1291).  One reciprocal and 64 multiplies measured
+    // 0.7% faster, with results up to 1 f16 ulp away: not the same operation.
     if constexpr (kSplit) {
         // Logical tile (q block, head group) = bq * (Hq/GROUP) + qh/GROUP; its
         // row r = (row % BM) * GROUP + qh % GROUP in split-major scratch
