@@ -680,13 +680,22 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
                         m_i[k] = mb;
                         const int nu = min(32, ns_b - sc);
                         if (nu == 32) {
+                            // All 32 row reads are issued before the arithmetic
+                            // (the fence keeps them together), so the chunk
+                            // pays one LDS latency instead of one per split.
+                            const unsigned char* xb = rbase + sc * G * 256;
+                            const int xstride = G * 256;
+                            half4_t xs[32];
+#pragma unroll
+                            for (int u = 0; u < 32; ++u)
+                                xs[u] = *reinterpret_cast<const half4_t*>(xb + u * xstride);
+                            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                             for (int u = 0; u < 32; ++u) {
                                 const float w = __builtin_amdgcn_exp2f(lv[u] - mb);
                                 s_i[k] += w;
-                                const half4_t x = *reinterpret_cast<const half4_t*>(rbase + (sc + u) * G * 256);
 #pragma unroll
-                                for (int e = 0; e < 4; ++e) acc[k][e] += w * static_cast<float>(x[e]);
+                                for (int e = 0; e < 4; ++e) acc[k][e] += w * static_cast<float>(xs[u][e]);
                             }
                         } else {
                             for (int u = 0; u < nu; ++u) {
