@@ -414,17 +414,15 @@ def bench_token_step(torch, ga, gen, layers=64, ctx=32768, steps=20):
 
 def bench_mfma_probe(torch, launches: int = 8):
     """Sustained v_mfma_f32_32x32x16_f16 rate for operand data distributed like the
-    prefill kernel's (grout_amd/probe/mfma_ceiling.hip), operands loaded once from
+    prefill kernel's (bench_probes/mfma_ceiling.hip), operands loaded once from
     16 MB f16 buffers: A ~ N(0,1) with B ~ N(0,1) (the Q K^T kind) or B = u1*u2 in
     [0,1) (the P V kind).  Returns TFLOP/s per kind and the rate of an equal mix of
     the two (harmonic mean: equal MFMA counts)."""
     import ctypes
 
-    from grout_amd import build as gbuild
+    import bench_probes
 
-    if not os.path.exists(gbuild.PROBE_LIB_PATH):
-        raise RuntimeError(f"{gbuild.PROBE_LIB_PATH} is not built; run `python -m grout_amd.build`")
-    lib = ctypes.CDLL(gbuild.PROBE_LIB_PATH)
+    lib = ctypes.CDLL(bench_probes.lib_path())
     fn = lib.grout_probe_mfma_f16
     fn.restype = ctypes.c_int32
     fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32,
@@ -461,14 +459,14 @@ def bench_mfma_probe(torch, launches: int = 8):
 
 
 def bench_hbm_probe(torch, gib: int = 4, launches: int = 5):
-    """Sustained HBM read rate of a plain streaming kernel (grout_amd/probe/hbm_read.hip)
+    """Sustained HBM read rate of a plain streaming kernel (bench_probes/hbm_read.hip)
     over a buffer far larger than the 256 MB last-level cache: the practical ceiling of the
     HBM-bound kernels.  GB/s (1e9 bytes)."""
     import ctypes
 
-    from grout_amd import build as gbuild
+    import bench_probes
 
-    lib = ctypes.CDLL(gbuild.PROBE_LIB_PATH)
+    lib = ctypes.CDLL(bench_probes.lib_path())
     fn = lib.grout_probe_hbm_read
     fn.restype = ctypes.c_int32
     fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
@@ -694,11 +692,11 @@ def main(argv=None) -> int:
             "unit": "TFLOP/s", "qk_operands": round(mp["qk"], 1), "pv_operands": round(mp["pv"], 1),
             "mix": round(mp["mix"], 1), "frac_of_nominal_peak": round(mp["mix"] / PEAK_TFLOPS_F16, 4),
             "prefill_frac_of_mix": round(pre["tflops"] / mp["mix"], 4),
-            "source": "grout_amd/probe/mfma_ceiling.hip"},
+            "source": "bench_probes/mfma_ceiling.hip"},
         # What a plain streaming read kernel sustains on this GPU (cache-cold, 4 GiB).
         "hbm_read_probe": {"unit": "GB/s", "value": round(hp["gbs"], 1),
                            "frac_of_peak": round(hp["gbs"] / PEAK_HBM_GBS, 4),
-                           "source": "grout_amd/probe/hbm_read.hip"},
+                           "source": "bench_probes/hbm_read.hip"},
         "decode": {
             "workload": "c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context 32768, "
                         f"hipGraph x{dec['replays']} of the fused step (norm/RoPE/KV write + "

@@ -442,7 +442,10 @@ class Qwen3DecodeRunner:
         return int(out.value)
 
     def run(self, first_position: int, count: int):
-        """`count` replays from `first_position`, each embedding the previous token."""
+        """`count` replays from `first_position`, each embedding the previous token.
+
+        Asynchronous on :attr:`stream`: synchronise it (or wait on an event
+        recorded on it) before reading logits, the token or the caches."""
         _check(lib().grout_qwen3_runner_run(self._h, int(first_position), int(count)),
                "qwen3_runner_run")
 
@@ -543,9 +546,9 @@ class DecodeGraphRunner:
     """Attention slice of DecodeCudaGraphRunner (src/model.rs:318-493).
 
     Captures the fused decode step (norm/RoPE/KV write, split-K decode, merge)
-    for one layer's buffers into a hipGraph; :meth:`launch_step` makes the
-    device position the requested one and replays it (no host sync).  The
-    graph advances the position itself, so consecutive steps write nothing."""
+    for one layer's buffers into a hipGraph; :meth:`launch_step` writes the
+    device position and replays it (no host sync); :meth:`run` writes it once
+    and lets each replay advance it."""
 
     def __init__(self, *, qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache,
                  att_partial, lse_partial, attn_out, position, eps: float,
@@ -577,11 +580,14 @@ class DecodeGraphRunner:
         self._h = h
 
     def launch_step(self, position: int):
+        """Writes the device position, then replays the graph, both on
+        :attr:`stream`; synchronise it before reading attn_out or the caches."""
         _check(lib().grout_decode_runner_step(self._h, int(position)), "decode_runner_step")
 
     def run(self, first_position: int, count: int):
         """`count` consecutive steps from `first_position`, issued from C without
-        returning to Python between steps (the graph advances the position)."""
+        returning to Python between steps (the graph advances the position).
+        Asynchronous on :attr:`stream`, as :meth:`launch_step`."""
         _check(lib().grout_decode_runner_run(self._h, int(first_position), int(count)),
                "decode_runner_run")
 

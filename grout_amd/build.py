@@ -2,9 +2,6 @@
 
 Usage: ``python -m grout_amd.build [--verbose]``.  Each ``csrc/*.hip`` file is
 compiled separately (in parallel) and linked into ``grout_amd/libgrout_attn_hip.so``.
-The measurement probe ``probe/*.hip`` (an MFMA-rate calibration bench.py
-reports beside the prefill roofline; not part of the C ABI) is linked into
-``grout_amd/libgrout_probe.so``.
 """
 from __future__ import annotations
 
@@ -20,8 +17,6 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libgrout_attn_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-PROBE_DIR = os.path.join(HERE, "probe")
-PROBE_LIB_PATH = os.path.join(HERE, "libgrout_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -79,15 +74,13 @@ def _link(objs: list[str], path: str, verbose: bool) -> None:
 
 
 def build(verbose: bool = False, extra: list[str] | None = None) -> str:
-    """Compile every csrc/*.hip (and probe/*.hip) for gfx950 and link the libraries."""
+    """Compile every csrc/*.hip for gfx950 and link the C-ABI library."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     extra = list(extra or [])
     srcs = sources()
-    probe_srcs = sources(PROBE_DIR)
-    with cf.ThreadPoolExecutor(max_workers=min(len(srcs) + len(probe_srcs), 8)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose, extra), srcs + probe_srcs))
-    _link(objs[:len(srcs)], LIB_PATH, verbose)
-    _link(objs[len(srcs):], PROBE_LIB_PATH, verbose)
+    with cf.ThreadPoolExecutor(max_workers=min(len(srcs), 8)) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose, extra), srcs))
+    _link(objs, LIB_PATH, verbose)
     return LIB_PATH
 
 

@@ -726,7 +726,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         if (tid == 0 && head_ticket == static_cast<uint32_t>(a.num_kv_heads) - 1u) {
             __hip_atomic_store(&a.counters[a.num_kv_heads * kDecCounterStride], 0u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.position_w, pos_raw + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // The position saturates at max_seq_len: a step at or past the end
+            // of the cache wrote no row and does not move it further.
+            if (pos_raw < static_cast<uint32_t>(a.max_seq_len))
+                __hip_atomic_store(a.position_w, pos_raw + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }

@@ -94,7 +94,6 @@ struct grout_qwen3_runner {
     std::vector<grout_qwen3_layer> layers;
     hipStream_t stream = nullptr;
     grout_graph* graph = nullptr;
-    uint32_t next_position = 0;
 };
 
 extern "C" int64_t grout_qwen3_workspace_bytes(const grout_qwen3_model* model) {
@@ -221,7 +220,6 @@ extern "C" int32_t grout_qwen3_runner_create(const grout_qwen3_model* model,
         return rec != GROUT_OK ? rec : st;
     }
     r->graph = g;
-    r->next_position = prime_position + 1;
     *runner = r;
     return GROUT_OK;
 }
@@ -238,13 +236,13 @@ extern "C" int32_t grout_qwen3_runner_step(grout_qwen3_runner* runner, uint32_t 
     GROUT_REQUIRE(runner != nullptr && runner->graph != nullptr, GROUT_ERR_GRAPH);
     GROUT_REQUIRE(position < static_cast<uint32_t>(runner->model.max_seq_len),
                   GROUT_ERR_SEQ_RANGE);
+    // launch_step writes the position on every step (src/model.rs:363-403):
+    // the device copy may have been moved outside the runner (an eager step,
+    // the caller).
     grout_stream_t gs = reinterpret_cast<grout_stream_t>(runner->stream);
-    int32_t st = GROUT_OK;
-    if (position != runner->next_position)
-        st = grout_set_position_async(runner->model.d_position, position, gs);
+    int32_t st = grout_set_position_async(runner->model.d_position, position, gs);
     if (st == GROUT_OK) st = grout_graph_launch(runner->graph, gs);
     if (st != GROUT_OK) return st;
-    runner->next_position = position + 1;
     if (token_out == nullptr) return GROUT_OK;
     // launch_step (src/model.rs:363-403): 4-byte read-back of the new token.
     hipError_t e = hipMemcpyAsync(token_out, runner->model.token, 4, hipMemcpyDeviceToHost,
@@ -261,18 +259,21 @@ extern "C" int32_t grout_qwen3_runner_run(grout_qwen3_runner* runner, uint32_t f
     GROUT_REQUIRE(static_cast<uint64_t>(first_position) + static_cast<uint64_t>(count) <=
                       static_cast<uint64_t>(runner->model.max_seq_len),
                   GROUT_ERR_SEQ_RANGE);
+    // The first step writes the position; each replay advances it in the
+    // graph and nothing else runs on the runner's stream in between.
     int32_t st = grout_qwen3_runner_step(runner, first_position, nullptr);
     grout_stream_t gs = reinterpret_cast<grout_stream_t>(runner->stream);
-    for (int32_t i = 1; st == GROUT_OK && i < count; ++i) {
-        st = grout_graph_launch(runner->graph, gs);
-        if (st == GROUT_OK) runner->next_position = first_position + static_cast<uint32_t>(i) + 1;
-    }
+    for (int32_t i = 1; st == GROUT_OK && i < count; ++i) st = grout_graph_launch(runner->graph, gs);
     return st;
 }
 
 extern "C" int32_t grout_qwen3_runner_destroy(grout_qwen3_runner* runner) {
     if (runner == nullptr) return GROUT_OK;
+    // Replays still queued on the runner's stream use the graph and the
+    // caller's buffers: let them finish first.
+    const hipError_t e = hipStreamSynchronize(runner->stream);
     const int32_t st = grout_graph_destroy(runner->graph);
     delete runner;
+    if (e != hipSuccess) return static_cast<int32_t>(e);
     return st;
 }

@@ -30,7 +30,6 @@ struct grout_decode_runner {
     grout_decode_layer layer;
     hipStream_t stream = nullptr;
     grout_graph* graph = nullptr;
-    uint32_t next_position = 0;  // device position left by the previous step
 };
 
 extern "C" const char* grout_status_string(int32_t status) {
@@ -177,7 +176,6 @@ extern "C" int32_t grout_decode_runner_create(const grout_decode_layer* layer,
     r->layer = L;
     r->stream = s;
     r->graph = g;
-    r->next_position = prime_position + 1;  // the prime pass advanced it
     *runner = r;
     return GROUT_OK;
 }
@@ -187,14 +185,13 @@ extern "C" int32_t grout_decode_runner_step(grout_decode_runner* runner, uint32_
     // src/model.rs:363-376 ensures the position fits; the cache bound is the
     // engine's max_seq_len.
     GROUT_REQUIRE(position < static_cast<uint32_t>(runner->layer.max_seq_len), GROUT_ERR_SEQ_RANGE);
+    // The position is written on every step, as launch_step does
+    // (src/model.rs:363-403): the device copy may have been moved by anything
+    // outside the runner (an eager step, the caller).
     grout_stream_t gs = reinterpret_cast<grout_stream_t>(runner->stream);
-    if (position != runner->next_position) {
-        const int32_t st = grout_set_position_async(runner->layer.d_position, position, gs);
-        if (st != GROUT_OK) return st;
-    }
-    const int32_t st = grout_graph_launch(runner->graph, gs);
-    if (st == GROUT_OK) runner->next_position = position + 1;
-    return st;
+    const int32_t st = grout_set_position_async(runner->layer.d_position, position, gs);
+    if (st != GROUT_OK) return st;
+    return grout_graph_launch(runner->graph, gs);
 }
 
 extern "C" int32_t grout_decode_runner_run(grout_decode_runner* runner, uint32_t first_position,
@@ -205,14 +202,12 @@ extern "C" int32_t grout_decode_runner_run(grout_decode_runner* runner, uint32_t
     GROUT_REQUIRE(static_cast<uint64_t>(first_position) + static_cast<uint64_t>(count) <=
                       static_cast<uint64_t>(runner->layer.max_seq_len),
                   GROUT_ERR_SEQ_RANGE);
-    // The first step positions the graph; every replay advances the device
-    // position itself, so the following replays need no host write.
+    // The first step writes the position; every replay advances the device
+    // position itself, and nothing else runs on the runner's stream in
+    // between, so the following replays need no host write.
     int32_t st = grout_decode_runner_step(runner, first_position);
     grout_stream_t gs = reinterpret_cast<grout_stream_t>(runner->stream);
-    for (int32_t i = 1; st == GROUT_OK && i < count; ++i) {
-        st = grout_graph_launch(runner->graph, gs);
-        if (st == GROUT_OK) runner->next_position = first_position + static_cast<uint32_t>(i) + 1;
-    }
+    for (int32_t i = 1; st == GROUT_OK && i < count; ++i) st = grout_graph_launch(runner->graph, gs);
     return st;
 }
 
@@ -228,7 +223,11 @@ extern "C" int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner) {
 
 extern "C" int32_t grout_decode_runner_destroy(grout_decode_runner* runner) {
     if (runner == nullptr) return GROUT_OK;
+    // Replays still queued on the runner's stream use the graph and the
+    // caller's buffers: let them finish first.
+    const hipError_t e = hipStreamSynchronize(runner->stream);
     int32_t st = grout_graph_destroy(runner->graph);
     delete runner;
+    if (e != hipSuccess) return static_cast<int32_t>(e);
     return st;
 }

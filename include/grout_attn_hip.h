@@ -273,7 +273,8 @@ int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_pa
  *   counters: grout_attn_decode_counter_bytes(num_kv_heads) bytes, zero
  *   before the first call; every call leaves them zero again.
  *   advance_position != 0: the launch ends by storing *d_position + 1, so a
- *   graph replayed once per token needs no position write in between.
+ *   graph replayed once per token needs no position write in between; a
+ *   position at or past max_seq_len (no cache row written) is left as it is.
  * Calls that overlap on one set of counters race. */
 int32_t grout_attn_decode_fused(const uint16_t* qkv, const uint16_t* q_weight,
                                 const uint16_t* k_weight, const float* inv_freq,
@@ -323,10 +324,13 @@ int32_t grout_set_position_async(uint32_t* d_position, uint32_t position,
 /* The attention slice of DecodeCudaGraphRunner (src/model.rs:318-493): one
  * hipGraph holding the fused decode step (grout_attn_decode_fused: QK
  * norm/RoPE/KV write, split-K decode, merge) for one layer's buffers,
- * replayed per token.  The graph advances the device position itself; a step
- * writes the position (stream-ordered) only when it is not the one the
- * previous step left.  All pointers are borrowed and must outlive the runner,
- * which owns *d_position and the counters while it lives. */
+ * replayed per token on the runner's stream.  Every step writes the position
+ * (stream-ordered) before its replay; the graph also advances it, which
+ * grout_decode_runner_run relies on between its replays.  Replays are
+ * asynchronous: synchronise the runner's stream (or wait on an event recorded
+ * on it) before reading attn_out, q_out or the caches.  All pointers are
+ * borrowed and must outlive the runner, which owns *d_position and the
+ * counters while it lives. */
 typedef struct grout_decode_layer {
     const uint16_t* qkv;       /* [(Hq + 2*Hkv) * 128] f16 QKV GEMV output */
     const uint16_t* q_weight;  /* [128] f16 */
@@ -355,9 +359,8 @@ typedef struct grout_decode_runner grout_decode_runner;
  * src/model.rs:2561-3115) at `prime_position`, then captures it. */
 int32_t grout_decode_runner_create(const grout_decode_layer* layer, uint32_t prime_position,
                                    grout_stream_t stream, grout_decode_runner** runner);
-/* launch_step (src/model.rs:363-403): make the device position `position`
- * (a stream-ordered write unless the previous step already left it there),
- * replay the graph.  No host sync. */
+/* launch_step (src/model.rs:363-403): stream-ordered write of the device
+ * position, then a replay of the graph.  No host sync. */
 int32_t grout_decode_runner_step(grout_decode_runner* runner, uint32_t position);
 /* `count` consecutive steps at positions first_position .. first_position+count-1
  * without returning to the caller in between: launch_step (src/model.rs:363-403)
@@ -369,6 +372,8 @@ int32_t grout_decode_runner_run(grout_decode_runner* runner, uint32_t first_posi
 /* zero_kv_caches (src/model.rs:433-462): clear both caches in place; pointers
  * stay valid for the captured graph.  Synchronises the runner's stream. */
 int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner);
+/* Waits for the runner's stream (queued replays use the borrowed buffers),
+ * then frees the graph. */
 int32_t grout_decode_runner_destroy(grout_decode_runner* runner);
 
 /* -------------------------------------- checkpoint formats (N4) */
@@ -448,15 +453,18 @@ int32_t grout_qwen3_runner_create(const grout_qwen3_model* model, uint32_t prime
                                   grout_stream_t stream, grout_qwen3_runner** runner);
 /* seed_token (src/model.rs:343-356): stream-ordered write of *token. */
 int32_t grout_qwen3_runner_seed_token(grout_qwen3_runner* runner, uint32_t token);
-/* launch_step (src/model.rs:363-403): position write unless the previous step
- * left it, graph replay; when token_out is not NULL, the new token is copied
- * back and the stream synchronised. */
+/* launch_step (src/model.rs:363-403): stream-ordered position write, graph
+ * replay; when token_out is not NULL, the new token is copied back and the
+ * stream synchronised. */
 int32_t grout_qwen3_runner_step(grout_qwen3_runner* runner, uint32_t position,
                                 uint32_t* token_out);
 /* `count` consecutive steps from first_position without host round trips
- * (each step embeds the token the previous one picked).  No host sync. */
+ * (each step embeds the token the previous one picked).  No host sync:
+ * synchronise the runner's stream before reading logits, *token or caches. */
 int32_t grout_qwen3_runner_run(grout_qwen3_runner* runner, uint32_t first_position,
                                int32_t count);
+/* Waits for the runner's stream (queued replays use the borrowed buffers),
+ * then frees the graph. */
 int32_t grout_qwen3_runner_destroy(grout_qwen3_runner* runner);
 /* A runner is used from one host thread at a time; two runners sharing a
  * workspace, token or position buffer race on the device. */

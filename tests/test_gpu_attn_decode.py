@@ -218,6 +218,12 @@ def _fused_case(seed, hq, hkv, MS):
     (64, 8, 2047, 2048, 32, 72),   # G = 8, last cache slot
     (4, 2, 0, 8, 4, 73),           # s_kv = 1, empty splits
     (16, 16, 300, 512, 3, 74),     # G = 1
+    # The in-kernel merge takes its partial rows in batches of 448 / G splits
+    # and carries (max, sum, acc) across them; these need 2-3 batches.
+    (32, 4, 4100, 4200, 64, 76),   # G = 8: batches of 56 splits (56 + 8)
+    (64, 4, 3000, 3100, 40, 77),   # G = 16: batches of 28 (28 + 12)
+    (48, 4, 4000, 4100, 75, 78),   # G = 12: batches of 37 (37 + 37 + 1)
+    (64, 4, 5000, 5100, 64, 79),   # G = 16: 28 + 28 + 8
 ])
 def test_fused_step_matches_oracle(gpu, hq, hkv, pos, MS, ns, seed):
     """grout_attn_decode_fused = norm/RoPE/KV write + split + merge of the oracle;
@@ -306,3 +312,35 @@ def test_fused_consecutive_steps_advance(gpu):
         assert_close_attn(out.cpu().numpy(), oracle.attn_decode_merge(a_ref, l_ref, G),
                           f"step {step}")
     assert int(dpos.item()) == p0 + 10
+
+
+def test_fused_position_saturates_past_cache(gpu):
+    """A fused step whose device position is at or past max_seq_len writes no
+    cache row and, with advance_position, leaves the position where it is; the
+    last slot itself (max_seq_len - 1) still advances to max_seq_len."""
+    import torch
+
+    import grout_amd
+    from tests._util import EPS, THETA
+
+    hq, hkv, MS, ns = 16, 4, 96, 3
+    _, qkv, qw, kw, kc, vc = _fused_case(80, hq, hkv, MS)
+    G = hq // hkv
+    inv = oracle.build_inv_freq(THETA)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    dkc, dvc = t(kc), t(vc)
+    q_out = torch.zeros(((hq + hkv), D), dtype=torch.float16, device="cuda")
+    out = torch.zeros((hkv, G, D), dtype=torch.float16, device="cuda")
+    att, lse = grout_amd.decode_scratch(hkv, G, ns)
+    counters = grout_amd.decode_counters(hkv)
+    for start, end in ((MS - 1, MS), (MS, MS), (MS + 5, MS + 5)):
+        dpos = torch.tensor([start], dtype=torch.int32, device="cuda")
+        before_k = dkc.clone()
+        grout_amd.decode_fused(t(qkv), t(qw), t(kw), t(inv), q_out, dkc, dvc, att, lse, out,
+                               counters, dpos, EPS, qk_scale_f16_bits(), hq, hkv,
+                               advance_position=True)
+        torch.cuda.synchronize()
+        assert int(dpos.item()) == end, f"position {start} -> {int(dpos.item())}"
+        assert int(counters.abs().sum().item()) == 0
+        if start >= MS:
+            assert torch.equal(before_k, dkc), "a position past the cache wrote a K row"

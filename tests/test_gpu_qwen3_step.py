@@ -212,3 +212,84 @@ def test_token_step_qwen3_06b_shapes(gpu):
         _check_caches(dm, ref, [30, 31, 32])
     finally:
         runner.close()
+
+
+def test_runner_step_after_eager_step_writes_position(gpu):
+    """step(p), an eager step (which moves the device position to p+2), then
+    step(p+1): the replay runs at p+1, as launch_step writes the position on
+    every step (src/model.rs:363-403).  Slot p+2 keeps its old contents."""
+    import torch
+    import grout_amd
+
+    m = qwen3_tiny_model(1700, layers=1, hidden=256, hq=8, hkv=2, inter=256, vocab=512,
+                         max_seq=64, filled=40)
+    ref = copy.deepcopy(m)
+    dm = _device_model(torch, m)
+    token = torch.tensor([9], dtype=torch.int32, device="cuda")
+    position = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    logits = torch.zeros((512,), dtype=torch.float16, device="cuda")
+    runner = grout_amd.Qwen3DecodeRunner(
+        **dm, token=token, position=position, logits=logits, num_q_heads=8, num_kv_heads=2,
+        eps=m["eps"], qk_scale_f16_bits=m["qk_scale_f16_bits"], num_splits=3, block_n=32,
+        prime_position=40)
+    try:
+        torch.cuda.synchronize()
+        # The oracle follows the token chain the GPU picked.
+        oracle.qwen3_decode_step(ref, 9, 40, 32, 3)
+        t_in = int(token.item())
+        runner.step(41)
+        oracle.qwen3_decode_step(ref, t_in, 41, 32, 3)
+        # Eager step at 41 + 1 = 42; the device position ends at 43.
+        t_in = int(token.item())
+        runner.eager_step()
+        runner.stream.synchronize()
+        assert int(position.item()) == 43
+        oracle.qwen3_decode_step(ref, t_in, 42, 32, 3)
+        # A step at 42 again: the runner must write the position.
+        t_in = int(token.item())
+        nxt = runner.step(42)
+        rl, _ = oracle.qwen3_decode_step(ref, t_in, 42, 32, 3)
+        gl = logits.cpu().numpy()
+        assert_close_attn(gl, rl, "step after eager step", atol=1e-2, rtol=1e-2)
+        assert nxt == oracle.argmax_f16(gl)
+        assert int(position.item()) == 43
+        _check_caches(dm, ref, [40, 41, 42])
+    finally:
+        runner.close()
+
+
+def test_runner_picked_splits_two_kv_heads_multi_batch_merge(gpu):
+    """A runner at Hkv=4, G=8 with grout_attn_decode_pick_splits' count (64 on
+    256 CUs): the fused merge folds its 64 splits in two batches of partial
+    rows, carrying the online max/sum across them."""
+    import torch
+    import grout_amd
+
+    m = qwen3_tiny_model(1750, layers=1, hidden=256, hq=32, hkv=4, inter=256, vocab=512,
+                         max_seq=4200, filled=4100)
+    ref = copy.deepcopy(m)
+    dm = _device_model(torch, m)
+    ns = grout_amd.pick_num_splits(4200, 4)
+    print(f"[qwen3 step] Hkv=4 G=8 picked splits {ns}", flush=True)
+    token = torch.tensor([3], dtype=torch.int32, device="cuda")
+    position = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    logits = torch.zeros((512,), dtype=torch.float16, device="cuda")
+    runner = grout_amd.Qwen3DecodeRunner(
+        **dm, token=token, position=position, logits=logits, num_q_heads=32, num_kv_heads=4,
+        eps=m["eps"], qk_scale_f16_bits=m["qk_scale_f16_bits"], num_splits=ns, block_n=32,
+        prime_position=4100)
+    try:
+        torch.cuda.synchronize()
+        rl, _ = oracle.qwen3_decode_step(ref, 3, 4100, 32, ns)
+        gl = logits.cpu().numpy()
+        assert_close_attn(gl, rl, "prime logits", atol=1e-2, rtol=1e-2)
+        tok = int(token.item())
+        assert tok == oracle.argmax_f16(gl)
+        nxt = runner.step(4101)
+        rl, _ = oracle.qwen3_decode_step(ref, tok, 4101, 32, ns)
+        gl = logits.cpu().numpy()
+        assert_close_attn(gl, rl, "replay logits", atol=1e-2, rtol=1e-2)
+        assert nxt == oracle.argmax_f16(gl)
+        _check_caches(dm, ref, [4100, 4101])
+    finally:
+        runner.close()
