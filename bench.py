@@ -8,17 +8,22 @@ fp16 dense MFMA peak, and decode attention GB/s as a fraction of HBM peak.
             32 Q / 8 KV heads, head_dim 128, f16 in / f32 accumulate.
             One step = one grout_attn_prefill launch; inputs already in HBM.
   decode  = config c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context
-            32768, {fused norm/RoPE/KV write, split-K decode, merge} captured
-            in a hipGraph and replayed 1000x with only the position updated.
-  also    = c3's fused QK norm/RoPE/KV write (HBM-bound) and c2 (Qwen3-4B
-            decode at context 4096).
+            32768, the fused {norm/RoPE/KV write, split-K decode, merge} step
+            captured in a hipGraph and replayed 1000x with only the position
+            updated; its roofline is the fused kernel with the KV caches of
+            four layers cycled (none resident in the 256 MB last-level cache).
+  also    = c1 (Qwen3-0.6B layer, S=512), c2 (Qwen3-4B decode at context
+            4096), c5 (Qwen3-32B prefill at S=32768 with 1% outlier keys,
+            unsplit and split-K, then 64 graph-replayed decode steps), the
+            Qwen3-4B decode at context 32768, c3's fused QK norm/RoPE/KV write,
+            the decode-layer ops and the whole Qwen3-32B token step.
 
-Kernel durations come from HIP events recorded on the launch stream: around
-each launch for prefill, and around a run of back-to-back launches (divided by
-the count) for the microsecond-scale decode and norm kernels, whose per-launch
-event pairs would add the launch latency.  The CPU baseline is the oracle (a C port of the reference's fp32
-CPU attention, benchmarks/src/bin/attention_microbench.rs:665-702) run on a
-bounded row sample of the same inputs.
+Kernel durations come from HIP events recorded on the launch stream, around a
+run of back-to-back launches divided by the count.  The CPU baseline is the
+oracle (a C restatement of the reference's fp32 CPU attention,
+benchmarks/src/bin/attention_microbench.rs:665-702) on the host's cores and on
+one thread, over stride samples of the same inputs (c5 extrapolated by the
+causal work ratio and labelled so).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -36,11 +41,13 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 # HIP runtime setting for the decode-graph replays, read when HIP initialises
-# (so before torch is imported): with the runtime's graph packet capture on, each
-# replay of the one-kernel decode graph costs ~4 us more GPU time than the same
-# kernel launched directly (measured 34.0 vs 30.2 us per step); with it off a
-# replay costs what a launch costs.  An explicit setting in the environment wins.
-GRAPH_PACKET_CAPTURE = os.environ.setdefault("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0")
+# (main() sets it before torch is imported): with the runtime's graph packet
+# capture on (its default), each replay of the one-kernel decode graph costs
+# ~4 us more GPU time than the same kernel launched directly; with it off a
+# replay costs what a launch costs.  An explicit setting in the environment
+# wins; bench.py also measures the c4 graph step under the runtime's default
+# in a child process (decode.graph_step_default_runtime_us).
+GRAPH_PACKET_ENV = "DEBUG_CLR_GRAPH_PACKET_CAPTURE"
 
 METRIC = ("prefill attn TFLOP/s (% fp16 MFMA peak); decode attn GB/s (% HBM peak), 1 GPU")
 PEAK_TFLOPS_F16 = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz (dense fp16 MFMA)
@@ -206,9 +213,12 @@ def bench_kv_update(torch, ga, steps, warmup, gen):
     return dict(ms=ms, bytes=nb, gbs=nb / (ms * 1e-3) / 1e9)
 
 
-def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
+def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps, graph_only=False,
+                 cold_caches=4):
     """Graph replay of {norm/RoPE/KV write, split, merge} at positions ctx..ctx+replays-1,
-    plus event-timed eager launches of the split kernel alone at position ctx."""
+    plus event-timed eager launches of the split kernel alone at position ctx.  The
+    caches-cycled figures rotate through `cold_caches` layers' caches, enough that no
+    launch finds its K/V in the 256 MB last-level cache."""
     G = hq // hkv
     MS = ctx + max(replays, 1024)
     kc = torch.randn((hkv, MS, D), device="cuda", generator=gen).half()
@@ -222,8 +232,7 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
     pos_t = torch.zeros((1,), device="cuda", dtype=torch.int32)
     ns = ga.pick_num_splits(MS, hkv)
     att, lse = ga.decode_scratch(hkv, G, ns)
-    scale_bits = int(torch.tensor([1.0 / math.sqrt(D)], dtype=torch.float16).view(torch.int16)
-                     .item()) & 0xFFFF
+    scale_bits = f16_scale_bits(torch)
     runner = ga.DecodeGraphRunner(
         qkv=qkv, q_weight=qw, k_weight=kw, inv_freq=inv, q_out=q_out, k_cache=kc, v_cache=vc,
         att_partial=att, lse_partial=lse, attn_out=attn_out, position=pos_t, eps=EPS,
@@ -246,6 +255,9 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
         runner.close()
     # Bytes of the average replayed step (s_kv grows by one per replay).
     avg_bytes = sum(decode_bytes(hq, hkv, ctx + i + 1) for i in range(replays)) / replays
+    if graph_only:
+        return dict(step_us=step_us, step_gbs=avg_bytes / (step_us * 1e-6) / 1e9,
+                    replays=replays)
 
     # The fused step alone (the graph's only kernel), eager at position ctx
     # (s_kv = ctx + 1, position not advanced), back-to-back launches; then the
@@ -259,26 +271,27 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps):
         q_grouped = q_out[:hq].view(hkv, G, D)
         fn = lambda: ga.fmha_decode_gqa_split(q_grouped, kc, vc, att, lse, scale_bits, pos_t)  # noqa
         split_us = 1e3 * time_back_to_back(torch, fn, split_steps, 10, stream=s)
-        # The same fused step cycling through 4 layers' caches (552 MB), so no
+        # The same fused step cycling through several layers' caches, so no
         # launch finds its K/V in the 256 MB last-level cache: the situation of
-        # a real token step, where 63 other layers run between two reads of one
-        # layer's cache.
-        kcs = [kc] + [torch.randn_like(kc) for _ in range(3)]
-        vcs = [vc] + [torch.randn_like(vc) for _ in range(3)]
+        # a real token step, where the other layers run between two reads of
+        # one layer's cache.
+        nc = cold_caches
+        kcs = [kc] + [torch.randn_like(kc) for _ in range(nc - 1)]
+        vcs = [vc] + [torch.randn_like(vc) for _ in range(nc - 1)]
         it = [0]
 
         def cold():
             it[0] += 1
-            c = it[0] % 4
+            c = it[0] % nc
             ga.decode_fused(qkv, qw, kw, inv, q_out, kcs[c], vcs[c], att, lse, attn_out,
                             counters, pos_t, EPS, scale_bits, hq, hkv)
-        cold_us = 1e3 * time_back_to_back(torch, cold, split_steps, 12, stream=s)
+        cold_us = 1e3 * time_back_to_back(torch, cold, split_steps, 3 * nc, stream=s)
 
         def split_cold():
             it[0] += 1
-            c = it[0] % 4
+            c = it[0] % nc
             ga.fmha_decode_gqa_split(q_grouped, kcs[c], vcs[c], att, lse, scale_bits, pos_t)
-        split_cold_us = 1e3 * time_back_to_back(torch, split_cold, split_steps, 12, stream=s)
+        split_cold_us = 1e3 * time_back_to_back(torch, split_cold, split_steps, 3 * nc, stream=s)
         del kcs, vcs
         mfn = lambda: ga.splitk_reduce_merge(att, lse, attn_out)  # noqa: E731
         # A ~4 us kernel launched back to back through the Python mirror is
@@ -490,40 +503,290 @@ def bench_hbm_probe(torch, gib: int = 4, launches: int = 5):
     return dict(gbs=gbs, bytes=nbytes, blocks=blocks)
 
 
-def cpu_baseline_prefill(torch, pre, threads: int):
-    """Oracle fp32 attention over every query row of the c3 inputs (about 10 s on 16 cores)."""
+def bench_prefill_c1(torch, ga, gen, n: int = 200):
+    """c1: Qwen3-0.6B layer, S=512, 16 Q / 8 KV heads: the fused QK norm/RoPE/KV
+    write, then causal prefill attention on the cache it wrote.  Both kernels
+    are a few microseconds, so each is timed over n back-to-back launches."""
+    hq, hkv, S = 16, 8, 512
+    q = torch.randn((S, hq, D), device="cuda", generator=gen).half()
+    k = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
+    v = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
+    qw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    kw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    inv = ga.build_inv_freq(THETA).cuda()
+    kc = torch.zeros((hkv, S, D), device="cuda", dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    qo = torch.empty_like(q)
+    out = torch.empty_like(q)
+    ga.qk_norm_rope_kv_prefill(q, k, v, qw, kw, inv, qo, kc, vc, EPS, 0)
+    ga.attend_prefill(qo, kc, vc, out, 0)
+    L = ga.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    nargs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), qw.data_ptr(), kw.data_ptr(),
+             inv.data_ptr(), qo.data_ptr(), kc.data_ptr(), vc.data_ptr(), EPS, 0, S, hq, hkv, D,
+             S, st)
+    pargs = (qo.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), 1.0 / math.sqrt(D),
+             hq, hkv, D, S, S, 0, S, st)
+    norm_ms = time_back_to_back(torch, lambda: L.grout_qk_norm_rope_kv_prefill(*nargs), n, 20)
+    attn_ms = time_back_to_back(torch, lambda: L.grout_attn_prefill(*pargs), n, 20)
+    assert torch.isfinite(out).all().item(), "non-finite c1 output"
+    flops = prefill_flops(hq, S)
+    nb = norm_bytes(hq, hkv, S)
+    return dict(attn_us=attn_ms * 1e3, tflops=flops / (attn_ms * 1e-3) / 1e12, flops=flops,
+                norm_us=norm_ms * 1e3, norm_gbs=nb / (norm_ms * 1e-3) / 1e9, norm_bytes=nb,
+                q=qo, kc=kc, vc=vc, hq=hq, hkv=hkv, S=S)
+
+
+def make_c5_inputs(torch, gen, hq=64, hkv=8, S=32768, extra=64):
+    """c5: Q/K/V ~ N(0,1) taken as post-norm/RoPE attention inputs, cache
+    [8, S + extra, 128]; 1% of the K rows of [0, S) scaled by 8 to stress the
+    online-softmax rescale."""
+    MS = S + extra
+    q = torch.randn((S, hq, D), device="cuda", generator=gen).half()
+    kc = torch.zeros((hkv, MS, D), device="cuda", dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    kc[:, :S].normal_(generator=gen)
+    vc[:, :S].normal_(generator=gen)
+    outlier = torch.rand((hkv, S), device="cuda", generator=gen) < 0.01
+    kc[:, :S][outlier] *= 8
+    return dict(q=q, kc=kc, vc=vc, hq=hq, hkv=hkv, S=S, MS=MS,
+                n_outlier_rows=int(outlier.sum().item()))
+
+
+def bench_c5(torch, ga, gen, steps: int = 5, warmup: int = 3, decode_steps: int = 64,
+             split=(2, 256, 64)):
+    """c5: Qwen3-32B causal prefill, S=32768, 64 Q / 8 KV heads, 1% of K rows x8;
+    the unsplit kernel and the split-K form (N3: NKS, BM, BN = `split`) on the
+    same inputs; then `decode_steps` graph-replayed decode steps appending to
+    the same cache (fused norm/RoPE/KV write + split-K + merge)."""
+    c5 = make_c5_inputs(torch, gen)
+    q, kc, vc, hq, hkv, S = c5["q"], c5["kc"], c5["vc"], c5["hq"], c5["hkv"], c5["S"]
+    out = torch.empty_like(q)
+    fn = lambda: ga.attend_prefill(q, kc, vc, out, 0)  # noqa: E731
+    ms, _ = time_region(torch, fn, steps, warmup)
+    assert torch.isfinite(out).all().item(), "non-finite c5 prefill output"
+    flops = prefill_flops(hq, S)
+    # Split-K prefill (fmha_prefill_gqa_lpt_split + merge) on the same inputs.
+    ns, bm, bn = split
+    gr = hq // hkv
+    att, lse = ga.prefill_split_scratch(hq, S, bm, gr, ns)
+    out_s = torch.empty_like(q)
+    sfn = lambda: ga.attend_prefill_split(q, kc, vc, att, lse, 0, bm, bn, gr, ns)  # noqa: E731
+    mfn = lambda: ga.prefill_splitk_reduce_merge(att, lse, out_s, bm, gr, ns)  # noqa: E731
+    split_ms, _ = time_region(torch, sfn, steps, 2)
+    merge_ms, _ = time_region(torch, mfn, steps, 2)
+    split_diff = (out_s.float() - out.float()).abs().max().item()
+    del att, lse, out_s
+    torch.cuda.empty_cache()
+
+    # 64 decode steps at positions S .. S+63 through the graph runner.
+    G = hq // hkv
+    qkv = torch.randn(((hq + 2 * hkv) * D,), device="cuda", generator=gen).half()
+    qw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    kw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    inv = ga.build_inv_freq(THETA).cuda()
+    q_out = torch.zeros(((hq + hkv), D), device="cuda", dtype=torch.float16)
+    attn_out = torch.zeros((hkv, G, D), device="cuda", dtype=torch.float16)
+    pos_t = torch.zeros((1,), device="cuda", dtype=torch.int32)
+    dns = ga.pick_num_splits(c5["MS"], hkv)
+    datt, dlse = ga.decode_scratch(hkv, G, dns)
+    runner = ga.DecodeGraphRunner(
+        qkv=qkv, q_weight=qw, k_weight=kw, inv_freq=inv, q_out=q_out, k_cache=kc, v_cache=vc,
+        att_partial=datt, lse_partial=dlse, attn_out=attn_out, position=pos_t, eps=EPS,
+        qk_scale_f16_bits=f16_scale_bits(torch), num_q_heads=hq, num_kv_heads=hkv,
+        num_splits=dns, prime_position=S)
+    s = runner.stream
+    try:
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        runner.run(S, decode_steps)
+        b.record(s)
+        torch.cuda.synchronize()
+        dec_us = a.elapsed_time(b) * 1e3 / decode_steps
+        assert int(pos_t.item()) == S + decode_steps
+        assert torch.isfinite(attn_out).all().item(), "non-finite c5 decode output"
+    finally:
+        runner.close()
+    dec_bytes = sum(decode_bytes(hq, hkv, S + i + 1) for i in range(decode_steps))
+    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, flops=flops, split_ms=split_ms,
+                merge_ms=merge_ms, split_tflops=flops / ((split_ms + merge_ms) * 1e-3) / 1e12,
+                split=split, split_max_diff=split_diff, decode_steps=decode_steps,
+                decode_us=dec_us, decode_bytes=dec_bytes,
+                decode_gbs=dec_bytes / decode_steps / (dec_us * 1e-6) / 1e9, decode_splits=dns,
+                n_outlier_rows=c5["n_outlier_rows"], inputs=c5)
+
+
+def f16_scale_bits(torch) -> int:
+    """f16::from_f32(1/sqrt(128)) (src/model.rs:3427)."""
+    return int(torch.tensor([1.0 / math.sqrt(D)], dtype=torch.float16).view(torch.int16)
+               .item()) & 0xFFFF
+
+
+def bench_decode_layers_graph(torch, ga, gen, hq, hkv, ctx, layers, replays):
+    """The fused decode step of `layers` layers (one KV cache each, together
+    larger than the 256 MB last-level cache) captured in one hipGraph, as in a
+    real token step where the other layers' caches pass between two reads of
+    one layer's: per-layer step time = replay time / layers.  Only the last
+    layer advances the position.  Returns microseconds per layer step."""
+    import ctypes
+
+    G = hq // hkv
+    MS = ctx + replays + 8
+    L = ga.lib()
+    caches = [(torch.empty((hkv, MS, D), device="cuda", dtype=torch.float16).normal_(generator=gen),
+               torch.empty((hkv, MS, D), device="cuda", dtype=torch.float16).normal_(generator=gen))
+              for _ in range(layers)]
+    qkv = torch.randn(((hq + 2 * hkv) * D,), device="cuda", generator=gen).half()
+    qw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    kw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    inv = ga.build_inv_freq(THETA).cuda()
+    q_out = torch.zeros(((hq + hkv), D), device="cuda", dtype=torch.float16)
+    attn_out = torch.zeros((hkv, G, D), device="cuda", dtype=torch.float16)
+    pos_t = torch.full((1,), ctx, device="cuda", dtype=torch.int32)
+    ns = ga.pick_num_splits(MS, hkv)
+    att, lse = ga.decode_scratch(hkv, G, ns)
+    counters = ga.decode_counters(hkv)
+    stream = torch.cuda.Stream()
+    sb = f16_scale_bits(torch)
+
+    def record():
+        for i, (kc, vc) in enumerate(caches):
+            st = L.grout_attn_decode_fused(
+                qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), inv.data_ptr(), q_out.data_ptr(),
+                kc.data_ptr(), vc.data_ptr(), att.data_ptr(), lse.data_ptr(), attn_out.data_ptr(),
+                counters.data_ptr(), pos_t.data_ptr(), EPS, sb, hq, hkv, D, MS, 32, ns,
+                1 if i == layers - 1 else 0, stream.cuda_stream)
+            assert st == 0, f"decode_fused status {st}"
+
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        record()  # eager prime pass: errors surface outside capture
+    stream.synchronize()
+    graph = ctypes.c_void_p()
+    assert L.grout_graph_begin(stream.cuda_stream) == 0
+    record()
+    assert L.grout_graph_end(stream.cuda_stream, ctypes.byref(graph)) == 0
+    try:
+        for _ in range(3):
+            assert L.grout_graph_launch(graph, stream.cuda_stream) == 0
+        stream.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(replays):
+            assert L.grout_graph_launch(graph, stream.cuda_stream) == 0
+        b.record(stream)
+        stream.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (replays * layers)
+        assert int(pos_t.item()) == ctx + 1 + 3 + replays
+    finally:
+        L.grout_graph_destroy(graph)
+    del caches
+    torch.cuda.empty_cache()
+    avg_bytes = decode_bytes(hq, hkv, ctx + 4 + (replays + 1) // 2)
+    return dict(us=us, gbs=avg_bytes / (us * 1e-6) / 1e9, layers=layers, replays=replays,
+                num_splits=ns)
+
+
+def host_threads():
+    """(threads used, host CPUs visible): all CPUs this process may run on,
+    capped by OMP_NUM_THREADS when it is set (the CPU share of a shared box)."""
+    visible = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    threads = min(visible, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else visible
+    return threads, visible
+
+
+def _cpu_prefill_rate(q, kc, vc, S, hq, query_start, kv_len, row_step, threads):
+    """The oracle's fp32 attention (cpu_reference restated) over query rows
+    0::row_step, all heads; returns (TFLOP/s, seconds, rows)."""
     import oracle
 
+    t0 = time.perf_counter()
+    oracle.attn_prefill_f32(q, kc, vc, 1.0 / math.sqrt(D), kv_len, query_start, row_begin=0,
+                            row_step=row_step, nthreads=threads)
+    dt = time.perf_counter() - t0
+    rows = range(0, S, row_step)
+    flops = sum(2.0 * 2.0 * D * hq * (query_start + m + 1) for m in rows)
+    return flops / dt / 1e12, dt, len(rows)
+
+
+def cpu_baselines(torch, pre, dec, c5, c1):
+    """The reference's CPU attention path (a C restatement of cpu_reference,
+    benchmarks/src/bin/attention_microbench.rs:665-702: fp32, two-pass softmax,
+    generalised to GQA on the cache and to decode) on this host, at all the
+    threads this process may use and at 1 thread, on bounded samples of the
+    configs' own inputs."""
+    import oracle
+
+    threads, visible = host_threads()
+    res = {"threads": threads, "host_cpus_visible": visible}
+    # c3 prefill: rows 0::2 on all threads, rows 0::32 on one.
     q = pre["q"].cpu().numpy()
     kc = pre["kc"].cpu().numpy()
     vc = pre["vc"].cpu().numpy()
     S, hq = pre["S"], pre["hq"]
-    step, begin = 1, 0
+    r_all, t_all, n_all = _cpu_prefill_rate(q, kc, vc, S, hq, 0, S, 2, threads)
+    r_one, t_one, n_one = _cpu_prefill_rate(q, kc, vc, S, hq, 0, S, 32, 1)
+    res["c3"] = dict(value=r_all, unit="TFLOP/s", cores=threads, single_thread_value=r_one,
+                     sample=f"c3 inputs, query rows 0::2 ({n_all} of {S}) x {hq} heads on "
+                            f"{threads} threads ({t_all:.1f} s); rows 0::32 ({n_one}) on 1 "
+                            f"thread ({t_one:.1f} s)")
+    del q, kc, vc
+    # c1 in full (norm output as the attention input), all threads and 1.
+    q1 = c1["q"].cpu().numpy()
+    k1 = c1["kc"].cpu().numpy()
+    v1 = c1["vc"].cpu().numpy()
+    r1, t1, _ = _cpu_prefill_rate(q1, k1, v1, c1["S"], c1["hq"], 0, c1["S"], 1, threads)
+    r1s, t1s, _ = _cpu_prefill_rate(q1, k1, v1, c1["S"], c1["hq"], 0, c1["S"], 1, 1)
+    res["c1"] = dict(value=r1, unit="TFLOP/s", cores=threads, single_thread_value=r1s,
+                     sample=f"c1 in full: {t1 * 1e3:.0f} ms on {threads} threads, "
+                            f"{t1s * 1e3:.0f} ms on 1")
+
+    # Decode steps: one c4 step (s_kv = ctx + 1) on all threads and on one.
+    def decode_rate(d, nthreads):
+        hq_, hkv_, ctx = d["hq"], d["hkv"], d["ctx"]
+        qd = d["q"].cpu().numpy().reshape(1, hq_, D)
+        kd = d["kc"][:, :ctx + 1].contiguous().cpu().numpy()
+        vd = d["vc"][:, :ctx + 1].contiguous().cpu().numpy()
+        t0 = time.perf_counter()
+        oracle.attn_prefill_f32(qd, kd, vd, 0.08837890625, ctx + 1, ctx, nthreads=nthreads)
+        dt = time.perf_counter() - t0
+        return decode_bytes(hq_, hkv_, ctx + 1) / dt / 1e9, dt
+
+    g_all, dt_all = decode_rate(dec, threads)
+    g_one, dt_one = decode_rate(dec, 1)
+    res["c4"] = dict(value=g_all, unit="GB/s", cores=threads, single_thread_value=g_one,
+                     sample=f"one c4 decode step (s_kv={dec['ctx'] + 1}, {dec['hq']} heads): "
+                            f"{dt_all * 1e3:.0f} ms on {threads} threads, {dt_one * 1e3:.0f} ms "
+                            "on 1")
+    # c5 prefill: rows 0::256 of all heads, extrapolated to the whole config by
+    # the exact causal work ratio; then its 64 decode steps in full.
+    inp = c5["inputs"]
+    q5 = inp["q"].cpu().numpy()
+    k5 = inp["kc"].cpu().numpy()
+    v5 = inp["vc"].cpu().numpy()
+    S5, hq5 = inp["S"], inp["hq"]
+    r5, t5, n5 = _cpu_prefill_rate(q5, k5, v5, S5, hq5, 0, S5, 256, threads)
+    full_s = c5["flops"] / (r5 * 1e12)
+    del q5
+    res["c5"] = dict(value=r5, unit="TFLOP/s", cores=threads, extrapolated=True,
+                     extrapolated_full_prefill_s=full_s,
+                     sample=f"c5 inputs, query rows 0::256 ({n5} of {S5}) x {hq5} heads on "
+                            f"{threads} threads ({t5:.1f} s), extrapolated to all rows by the "
+                            "causal work ratio")
+    qd = torch.randn((1, hq5, D), generator=torch.Generator().manual_seed(5)).half().numpy()
     t0 = time.perf_counter()
-    oracle.attn_prefill_f32(q, kc, vc, 1.0 / math.sqrt(D), S, 0, row_begin=begin,
-                            row_step=step, nthreads=threads)
+    for i in range(c5["decode_steps"]):
+        oracle.attn_prefill_f32(qd, k5, v5, 0.08837890625, S5 + i + 1, S5 + i, nthreads=threads)
     dt = time.perf_counter() - t0
-    rows = range(begin, S, step)
-    flops = sum(2.0 * 2.0 * D * hq * (m + 1) for m in rows)
-    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"c3 inputs, query rows {begin}::{step} ({len(rows)} of {S}) x {hq} "
-                       f"heads, {dt:.1f} s; oracle/grout_oracle.c go_attn_prefill_f32 "
-                       f"(fp32, two-pass softmax), OpenMP over (row, head)")
-
-
-def cpu_baseline_decode(torch, dec, threads: int):
-    import oracle
-
-    hq, hkv, ctx = dec["hq"], dec["hkv"], dec["ctx"]
-    q = dec["q"].cpu().numpy().reshape(1, hq, D)
-    kc = dec["kc"][:, :ctx + 1].contiguous().cpu().numpy()
-    vc = dec["vc"][:, :ctx + 1].contiguous().cpu().numpy()
-    t0 = time.perf_counter()
-    oracle.attn_prefill_f32(q, kc, vc, 0.08837890625, ctx + 1, ctx, nthreads=threads)
-    dt = time.perf_counter() - t0
-    return dict(value=decode_bytes(hq, hkv, ctx + 1) / dt / 1e9, unit="GB/s", cores=threads,
-                kind="port", sample=f"one c4 decode step (s_kv={ctx + 1}, {hq} heads), "
-                                    f"{dt * 1e3:.0f} ms, fp32 oracle")
+    res["c5_decode"] = dict(value=c5["decode_bytes"] / dt / 1e9, unit="GB/s", cores=threads,
+                            sample=f"c5's {c5['decode_steps']} decode steps in full "
+                                   f"(s_kv {S5 + 1}..{S5 + c5['decode_steps']}): {dt:.1f} s on "
+                                   f"{threads} threads")
+    return res
 
 
 def main(argv=None) -> int:
@@ -537,9 +800,13 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-replays", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "prefill", "prefill-split", "decode", "norm", "kv",
-                                       "mfma-probe", "decode-layer", "token-step", "hbm-probe"],
+                                       "mfma-probe", "decode-layer", "token-step", "hbm-probe",
+                                       "c1", "c5", "decode-graph-step"],
                     default="all",
-                    help="run one workload only (for profiling runs); prints no JSON line")
+                    help="run one workload only (for profiling runs); prints no JSON line "
+                         "(decode-graph-step prints the c4 graph step as one JSON line)")
+    ap.add_argument("--hip-default-graph-capture", action="store_true",
+                    help=f"leave {GRAPH_PACKET_ENV} unset (the HIP runtime's default)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (reads and writes 1 GiB) "
                          "to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings, then exit")
@@ -549,6 +816,9 @@ def main(argv=None) -> int:
               "(attention shards by KV head with no communication; see DESIGN.md).",
               file=sys.stderr)
         return 2
+    if not args.hip_default_graph_capture:
+        os.environ.setdefault(GRAPH_PACKET_ENV, "0")
+    packet_capture = os.environ.get(GRAPH_PACKET_ENV, "runtime default")
 
     import torch
 
@@ -605,6 +875,22 @@ def main(argv=None) -> int:
             mp = bench_mfma_probe(torch)
             log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
                 f"mix {mp['mix']:.0f} TFLOP/s")
+        elif args.only == "c1":
+            c1 = bench_prefill_c1(torch, ga, gen)
+            log(f"c1: attention {c1['attn_us']:.2f} us ({c1['tflops']:.1f} TFLOP/s), norm "
+                f"{c1['norm_us']:.2f} us ({c1['norm_gbs']:.0f} GB/s)")
+        elif args.only == "c5":
+            c5 = bench_c5(torch, ga, gen, steps=args.steps, warmup=min(args.warmup, 5))
+            log(f"c5: prefill {c5['ms']:.2f} ms ({c5['tflops']:.1f} TFLOP/s); split-K "
+                f"{c5['split_ms']:.2f} + {c5['merge_ms']:.2f} ms; decode {c5['decode_us']:.2f} "
+                f"us/step")
+        elif args.only == "decode-graph-step":
+            dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, 20, gen, 200,
+                               graph_only=True)
+            print(json.dumps({"graph_step_us": round(dec["step_us"], 3),
+                              "graph_step_gbs": round(dec["step_gbs"], 1),
+                              "replays": dec["replays"], "packet_capture": packet_capture}),
+                  flush=True)
         else:
             dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, args.warmup, gen,
                                args.steps)
@@ -626,19 +912,41 @@ def main(argv=None) -> int:
         f"mix {mp['mix']:.0f} TFLOP/s; prefill = {pre['tflops'] / mp['mix']:.3f} of the mix")
     hp = bench_hbm_probe(torch)
     log(f"hbm read probe: {hp['gbs']:.0f} GB/s over {hp['bytes'] >> 30} GiB")
+    log("c1 ...")
+    c1 = bench_prefill_c1(torch, ga, gen)
+    log(f"c1: attention {c1['attn_us']:.2f} us ({c1['tflops']:.1f} TFLOP/s), norm "
+        f"{c1['norm_us']:.2f} us ({c1['norm_gbs']:.0f} GB/s)")
     log("qk_norm_rope c3 ...")
     nrm = bench_norm(torch, ga, args.steps, args.warmup, gen)
     log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
     kvu = bench_kv_update(torch, ga, args.steps, args.warmup, gen)
     log(f"kv update c3: {kvu['ms'] * 1e3:.1f} us, {kvu['gbs']:.0f} GB/s")
+    log("c5 ...")
+    c5 = bench_c5(torch, ga, gen)
+    log(f"c5: prefill {c5['ms']:.2f} ms ({c5['tflops']:.1f} TFLOP/s); split-K "
+        f"{c5['split_ms']:.2f} + {c5['merge_ms']:.2f} ms ({c5['split_tflops']:.1f} TFLOP/s); "
+        f"{c5['decode_steps']} decode steps {c5['decode_us']:.2f} us/step "
+        f"({c5['decode_gbs']:.0f} GB/s)")
     log("decode c4 ...")
     dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, 20, gen, 200)
-    log(f"decode c4: graph step {dec['step_us']:.2f} us ({dec['step_gbs']:.0f} GB/s), "
-        f"fused kernel {dec['fused_us']:.2f} us ({dec['fused_gbs']:.0f} GB/s; "
-        f"caches cycled {dec['cold_us']:.2f} us, {dec['cold_gbs']:.0f} GB/s), "
-        f"split {dec['split_us']:.2f} us ({dec['split_gbs']:.0f} GB/s; caches cycled "
-        f"{dec['split_cold_us']:.2f} us), "
-        f"merge {dec['merge_us']:.2f} us, NKS={dec['num_splits']}")
+    dec_layers = bench_decode_layers_graph(torch, ga, gen, 64, 8, 32768, 4, 100)
+    log(f"decode c4: graph step {dec['step_us']:.2f} us ({dec['step_gbs']:.0f} GB/s); 4-layer "
+        f"graph {dec_layers['us']:.2f} us/layer ({dec_layers['gbs']:.0f} GB/s); fused kernel "
+        f"{dec['fused_us']:.2f} us (caches cycled {dec['cold_us']:.2f} us, "
+        f"{dec['cold_gbs']:.0f} GB/s); split {dec['split_us']:.2f} us (caches cycled "
+        f"{dec['split_cold_us']:.2f} us); merge {dec['merge_us']:.2f} us, NKS={dec['num_splits']}")
+    graph_default = measure_graph_step_default_runtime(args.decode_replays, log)
+    log("decode Qwen3-4B 32K ...")
+    dec4b = bench_decode(torch, ga, 32, 8, 32768, 200, 20, gen, 200)
+    dec4b_layers = bench_decode_layers_graph(torch, ga, gen, 32, 8, 32768, 4, 100)
+    log(f"decode 4B ctx 32768: fused kernel caches cycled {dec4b['cold_us']:.2f} us "
+        f"({dec4b['cold_gbs']:.0f} GB/s), 4-layer graph {dec4b_layers['us']:.2f} us/layer")
+    log("decode c2 ...")
+    dec2 = bench_decode(torch, ga, 32, 8, 4096, 200, 20, gen, 200, cold_caches=24)
+    dec2_layers = bench_decode_layers_graph(torch, ga, gen, 32, 8, 4096, 24, 40)
+    log(f"decode c2: graph step {dec2['step_us']:.2f} us, fused {dec2['fused_us']:.2f} us "
+        f"(caches cycled {dec2['cold_us']:.2f} us), split {dec2['split_us']:.2f} us, 24-layer "
+        f"graph {dec2_layers['us']:.2f} us/layer")
     log("decode layer ops c4 ...")
     dl = bench_decode_layer(torch, ga, args.steps, gen)
     log("decode layer c4: " + ", ".join(
@@ -648,23 +956,27 @@ def main(argv=None) -> int:
     ts = bench_token_step(torch, ga, gen)
     log(f"token step c4 ({ts['layers']} layers, ctx {ts['ctx']}): {ts['ms']:.3f} ms/token, "
         f"{ts['tokens_per_s']:.1f} tok/s, {ts['gbs']:.0f} GB/s")
-    log("decode c2 ...")
-    dec2 = bench_decode(torch, ga, 32, 8, 4096, 200, 20, gen, 200)
-    log(f"decode c2: graph step {dec2['step_us']:.2f} us, fused {dec2['fused_us']:.2f} us, "
-        f"split {dec2['split_us']:.2f} us")
 
-    threads = min(16, os.cpu_count() or 1)
     cpu = None
-    cpu_dec = None
     if not args.no_cpu_baseline:
-        log(f"cpu baseline ({threads} threads) ...")
-        cpu = cpu_baseline_prefill(torch, pre, threads)
-        cpu_dec = cpu_baseline_decode(torch, dec, threads)
-        log(f"cpu: {cpu['value'] * 1e3:.2f} GFLOP/s prefill, {cpu_dec['value']:.2f} GB/s decode")
+        threads, visible = host_threads()
+        log(f"cpu baseline ({threads} threads of {visible} visible, and 1 thread) ...")
+        cpu = cpu_baselines(torch, pre, dec, c5, c1)
+        log(f"cpu: c3 {cpu['c3']['value'] * 1e3:.2f} GFLOP/s ({cpu['c3']['single_thread_value'] * 1e3:.2f} "
+            f"on 1 thread), c4 {cpu['c4']['value']:.2f} GB/s, c5 {cpu['c5']['value'] * 1e3:.2f} "
+            f"GFLOP/s (extrapolated), c5 decode {cpu['c5_decode']['value']:.2f} GB/s")
 
     def rl(bound, achieved, peak, unit, traffic=None):
         return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                 "frac": round(achieved / peak, 4), "traffic": traffic}
+
+    def cpu_entry(key):
+        if cpu is None:
+            return None
+        e = dict(cpu[key])
+        e.setdefault("kind", "port")
+        e["host_cpus_visible"] = cpu["host_cpus_visible"]
+        return {k: (round(v, 6) if isinstance(v, float) else v) for k, v in e.items()}
 
     line = {
         "metric": METRIC,
@@ -685,7 +997,7 @@ def main(argv=None) -> int:
                    "head_dim": D, "flops_per_step": pre["flops"]},
         "roofline": rl("mfma", pre["tflops"], PEAK_TFLOPS_F16, "TFLOP/s",
                        traffic=round(PMC_TRAFFIC_BYTES["attn_prefill_c3"])),
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_entry("c3"),
         # What the matrix cores sustain on this GPU for operands distributed like
         # the prefill kernel's (MFMAs only, no memory or softmax work).
         "mfma_ceiling_probe": {
@@ -703,30 +1015,80 @@ def main(argv=None) -> int:
                         "split + merge, one kernel)",
             "value": round(dec["step_gbs"], 1), "unit": "GB/s",
             "us_per_step": round(dec["step_us"], 3), "num_splits": dec["num_splits"],
-            "fused_kernel_us": round(dec["fused_us"], 3),
+            # The roofline is the fused kernel with four layers' caches cycled
+            # (none served from the 256 MB last-level cache), as in a token step.
+            "roofline": rl("hbm", dec["cold_gbs"], PEAK_HBM_GBS, "GB/s",
+                           traffic=round(PMC_TRAFFIC_BYTES["attn_decode_fused_c4"])),
             "fused_kernel_cold_cache_us": round(dec["cold_us"], 3),
-            "fused_kernel_cold_cache_gbs": round(dec["cold_gbs"], 1),
+            "fused_kernel_warm_us": round(dec["fused_us"], 3),
+            "graph_step_cold_cache_us": round(dec_layers["us"], 3),
+            "graph_step_cold_cache_gbs": round(dec_layers["gbs"], 1),
+            "graph_step_cold_cache_frac_of_hbm_peak": round(dec_layers["gbs"] / PEAK_HBM_GBS, 4),
+            "graph_step_cold_cache_note": "4 layers' fused steps (4 caches, 552 MB) in one "
+                                          "hipGraph, replay time / 4",
+            "graph_step_default_runtime_us": graph_default,
+            "hip_graph_packet_capture": packet_capture,
             "standalone_split_us": round(dec["split_us"], 3),
             "standalone_split_cold_cache_us": round(dec["split_cold_us"], 3),
             "standalone_split_cold_cache_frac_of_hbm_peak": round(
                 dec["bytes_step"] / (dec["split_cold_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "standalone_merge_us": round(dec["merge_us"], 3),
-            "roofline": rl("hbm", dec["fused_gbs"], PEAK_HBM_GBS, "GB/s",
-                           traffic=round(PMC_TRAFFIC_BYTES["attn_decode_fused_c4"])),
             "step_frac_of_hbm_peak": round(dec["step_gbs"] / PEAK_HBM_GBS, 4),
-            "fused_kernel_frac_of_read_probe": round(dec["fused_gbs"] / hp["gbs"], 4),
-            "hip_graph_packet_capture": GRAPH_PACKET_CAPTURE,
-            "cpu_baseline": cpu_dec,
+            "fused_kernel_cold_cache_frac_of_read_probe": round(dec["cold_gbs"] / hp["gbs"], 4),
+            "cpu_baseline": cpu_entry("c4"),
         },
+        "decode_qwen3_4b_32k": {
+            "workload": "Qwen3-4B decode step (32 Q / 8 KV heads), context 32768: the north "
+                        "star's decode target shape",
+            "fused_kernel_cold_cache_us": round(dec4b["cold_us"], 3),
+            "roofline": rl("hbm", dec4b["cold_gbs"], PEAK_HBM_GBS, "GB/s"),
+            "graph_step_cold_cache_us": round(dec4b_layers["us"], 3),
+            "graph_step_cold_cache_frac_of_hbm_peak": round(dec4b_layers["gbs"] / PEAK_HBM_GBS, 4),
+            "graph_step_warm_us": round(dec4b["step_us"], 3),
+            "num_splits": dec4b["num_splits"]},
+        "c5": {
+            "workload": "Qwen3-32B causal prefill, S=32768, 64 Q / 8 KV heads, 1% of K rows x8, "
+                        f"then {c5['decode_steps']} graph-replayed decode steps on the same cache",
+            "prefill_ms": round(c5["ms"], 3),
+            "roofline": rl("mfma", c5["tflops"], PEAK_TFLOPS_F16, "TFLOP/s"),
+            "prefill_flops": c5["flops"], "outlier_k_rows": c5["n_outlier_rows"],
+            "split_k": {"num_splits": c5["split"][0], "block_m": c5["split"][1],
+                        "block_n": c5["split"][2], "split_ms": round(c5["split_ms"], 3),
+                        "merge_ms": round(c5["merge_ms"], 3),
+                        "TFLOP/s": round(c5["split_tflops"], 1),
+                        "vs_unsplit": round(c5["ms"] / (c5["split_ms"] + c5["merge_ms"]), 4),
+                        "max_abs_diff_vs_unsplit": c5["split_max_diff"]},
+            "decode_us_per_step": round(c5["decode_us"], 3),
+            "decode_roofline": rl("hbm", c5["decode_gbs"], PEAK_HBM_GBS, "GB/s"),
+            "decode_num_splits": c5["decode_splits"],
+            "cpu_baseline": cpu_entry("c5"),
+            "cpu_baseline_decode": cpu_entry("c5_decode"),
+        },
+        "c1": {
+            "workload": "Qwen3-0.6B layer, S=512, 16 Q / 8 KV heads: fused QK norm/RoPE/KV "
+                        "write then causal prefill attention (launch-bound sizes)",
+            "attn_us": round(c1["attn_us"], 3),
+            "roofline": rl("mfma", c1["tflops"], PEAK_TFLOPS_F16, "TFLOP/s"),
+            "norm_us": round(c1["norm_us"], 3),
+            "norm_roofline": rl("hbm", c1["norm_gbs"], PEAK_HBM_GBS, "GB/s"),
+            "cpu_baseline": cpu_entry("c1"),
+        },
+        "decode_c2": {
+            "workload": "c2: Qwen3-4B decode step, 32 Q / 8 KV heads, context 4096",
+            "us_per_step": round(dec2["step_us"], 3),
+            "fused_kernel_warm_us": round(dec2["fused_us"], 3),
+            "fused_kernel_cold_cache_us": round(dec2["cold_us"], 3),
+            "roofline": rl("hbm", dec2["cold_gbs"], PEAK_HBM_GBS, "GB/s"),
+            "graph_step_cold_cache_us": round(dec2_layers["us"], 3),
+            "graph_step_cold_cache_note": "24 layers' fused steps in one hipGraph, replay "
+                                          "time / 24",
+            "standalone_split_us": round(dec2["split_us"], 3),
+            "num_splits": dec2["num_splits"]},
         "prefill_split_c3": {
             "split_us": round(psp["ms"] * 1e3, 2), "merge_us": round(psp["merge_ms"] * 1e3, 2),
             "TFLOP/s": round(psp["tflops"], 1), "num_splits": psp["num_splits"],
             "block_m": psp["block_m"], "block_n": psp["block_n"], "group": psp["group"],
             "max_abs_diff_vs_unsplit": psp["max_diff_vs_unsplit"]},
-        "decode_c2": {"us_per_step": round(dec2["step_us"], 3),
-                      "fused_kernel_us": round(dec2["fused_us"], 3),
-                      "fused_gbs": round(dec2["fused_gbs"], 1),
-                      "num_splits": dec2["num_splits"]},
         "decode_layer_c4": {
             **{nm: {"m": dl[nm]["m"], "k": dl[nm]["k"], "us": round(dl[nm]["us"], 2),
                     "GB/s": round(dl[nm]["gbs"], 1),
@@ -749,6 +1111,28 @@ def main(argv=None) -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def measure_graph_step_default_runtime(replays: int, log):
+    """The c4 graph step (1000 replays of the one-kernel graph) under the HIP
+    runtime's default graph packet capture: the setting is read when HIP
+    initialises, so this runs bench.py once more as a child process with the
+    variable removed from its environment.  Returns microseconds per step, or
+    None when the child fails (its output is logged)."""
+    import subprocess
+
+    env = dict(os.environ)
+    env.pop(GRAPH_PACKET_ENV, None)
+    cmd = [sys.executable, os.path.abspath(__file__), "--only", "decode-graph-step",
+           "--hip-default-graph-capture", "--decode-replays", str(replays)]
+    r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=300)
+    for ln in r.stdout.splitlines()[::-1]:
+        if ln.startswith("{"):
+            v = json.loads(ln)["graph_step_us"]
+            log(f"c4 graph step with the HIP runtime's default graph capture: {v:.2f} us")
+            return v
+    log(f"default-runtime graph step failed (rc {r.returncode}): {r.stderr[-400:]}")
+    return None
 
 
 if __name__ == "__main__":
