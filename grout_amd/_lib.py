@@ -31,6 +31,7 @@ STATUS_NAMES = {
     -8: "GROUT_ERR_SPLITS",
     -9: "GROUT_ERR_ARG",
     -10: "GROUT_ERR_GRAPH",
+    -11: "GROUT_ERR_SCRATCH",
 }
 NAME_TO_STATUS = {v: k for k, v in STATUS_NAMES.items()}
 
@@ -102,6 +103,8 @@ SIGNATURES = {
     "grout_attn_decode_merge": (c_i32, [c_vp] * 3 + [c_i32] * 4 + [c_vp]),
     "grout_attn_decode_fused": (
         c_i32, [c_vp] * 12 + [c_f32, c_u16] + [c_i32] * 7 + [c_vp]),
+    "grout_attn_decode_fused_noalloc": (
+        c_i32, [c_vp] * 9 + [c_f32, c_u16] + [c_i32] * 7 + [c_vp]),
     "grout_attn_decode_counter_bytes": (c_i64, [c_i32]),
     "grout_attn_decode_partial_bytes": (c_i64, [c_i32] * 4),
     "grout_attn_decode_lse_bytes": (c_i64, [c_i32] * 3),

@@ -40,6 +40,8 @@
 //    the last KV head to complete advances the device position.
 #include <math.h>
 
+#include <mutex>
+
 #include "abi_util.h"
 #include "common.h"
 
@@ -850,7 +852,7 @@ extern "C" int32_t grout_attn_decode_split(const uint16_t* q, const uint16_t* k_
     return launch_status();
 }
 
-extern "C" int32_t grout_attn_decode_fused(
+static int32_t fused_decode(
     const uint16_t* qkv, const uint16_t* q_weight, const uint16_t* k_weight,
     const float* inv_freq, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
     uint16_t* att_partial, float* lse_partial, uint16_t* out, uint32_t* counters,
@@ -901,6 +903,96 @@ extern "C" int32_t grout_attn_decode_fused(
     hipLaunchKernelGGL(attn_decode_kernel<true>, dim3(num_splits, num_kv_heads), dim3(kDecThreads),
                        0, to_hip(stream), a);
     return launch_status();
+}
+
+extern "C" int32_t grout_attn_decode_fused(
+    const uint16_t* qkv, const uint16_t* q_weight, const uint16_t* k_weight,
+    const float* inv_freq, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+    uint16_t* att_partial, float* lse_partial, uint16_t* out, uint32_t* counters,
+    uint32_t* d_position, float eps, uint16_t qk_scale_f16, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len, int32_t block_n,
+    int32_t num_splits, int32_t advance_position, grout_stream_t stream) {
+    return fused_decode(qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache, att_partial,
+                        lse_partial, out, counters, d_position, eps, qk_scale_f16, num_q_heads,
+                        num_kv_heads, head_dim, max_seq_len, block_n, num_splits,
+                        advance_position, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free fused decode: the same kernel with its split partials, LSEs
+// and merge counters in a static device array instead of caller buffers.
+//
+// Layout of `scratch`: [0, 64 KiB) merge counters (kDecCounterStride apart, one
+// 256-byte line per KV head plus the head counter), then the LSEs (f32, one
+// per (kv_head, split, g) row), then the partial rows (f16, 256 B each) from
+// the next 256-byte boundary.
+constexpr size_t kNoAllocBytes = static_cast<size_t>(GROUT_NOALLOC_SCRATCH_BYTES);
+constexpr size_t kNoAllocCounterBytes = 64 * 1024;
+static_assert(kNoAllocCounterBytes ==
+                  static_cast<size_t>(GROUT_NOALLOC_MAX_KV_HEADS + 1) * kDecCounterStride * 4,
+              "one counter line per KV head plus the head counter");
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+__global__ void zero_u32_kernel(uint32_t* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+namespace {
+
+// Per-device address of `scratch` (the name is only a host-side stand-in):
+// looked up once per device with that device current, then used for every
+// kernel argument.
+struct NoAllocDevice {
+    std::once_flag once;
+    unsigned char* ptr = nullptr;
+    int32_t status = GROUT_OK;
+};
+constexpr int kNoAllocMaxDevices = 64;
+NoAllocDevice g_noalloc[kNoAllocMaxDevices];
+
+}  // namespace
+
+extern "C" int32_t grout_attn_decode_fused_noalloc(
+    const uint16_t* qkv, const uint16_t* q_weight, const uint16_t* k_weight,
+    const float* inv_freq, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, uint16_t* out,
+    uint32_t* d_position, float eps, uint16_t qk_scale_f16, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len, int32_t block_n,
+    int32_t num_splits, int32_t advance_position, grout_stream_t stream) {
+    GROUT_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
+                  GROUT_ERR_HEADS);
+    GROUT_REQUIRE(num_splits >= 1 && num_splits <= GROUT_MAX_DECODE_SPLITS, GROUT_ERR_SPLITS);
+    GROUT_REQUIRE(num_kv_heads <= GROUT_NOALLOC_MAX_KV_HEADS, GROUT_ERR_SCRATCH);
+    const int64_t rows = static_cast<int64_t>(num_q_heads) * num_splits;  // Hkv * NS * G
+    const int64_t lse_bytes = (rows * 4 + 255) & ~static_cast<int64_t>(255);
+    const int64_t need = static_cast<int64_t>(kNoAllocCounterBytes) + lse_bytes + rows * kHeadDim * 2;
+    GROUT_REQUIRE(need <= static_cast<int64_t>(kNoAllocBytes), GROUT_ERR_SCRATCH);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return static_cast<int32_t>(e);
+    GROUT_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices, GROUT_ERR_SCRATCH);
+    NoAllocDevice& d = g_noalloc[dev];
+    // Set-up, once per device: the array's address on this device, and its
+    // counters cleared in stream order (every launch leaves them zero again).
+    std::call_once(d.once, [&] {
+        void* p = nullptr;
+        const hipError_t ge = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (ge != hipSuccess) {
+            d.status = static_cast<int32_t>(ge);
+            return;
+        }
+        d.ptr = static_cast<unsigned char*>(p);
+        constexpr int n = static_cast<int>(kNoAllocCounterBytes / 4);
+        hipLaunchKernelGGL(zero_u32_kernel, dim3(16), dim3(256), 0, to_hip(stream),
+                           reinterpret_cast<uint32_t*>(d.ptr), n);
+        d.status = launch_status();
+    });
+    if (d.status != GROUT_OK) return d.status;
+    uint32_t* counters = reinterpret_cast<uint32_t*>(d.ptr);
+    float* lse = reinterpret_cast<float*>(d.ptr + kNoAllocCounterBytes);
+    uint16_t* att = reinterpret_cast<uint16_t*>(d.ptr + kNoAllocCounterBytes + lse_bytes);
+    return fused_decode(qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache, att, lse, out,
+                        counters, d_position, eps, qk_scale_f16, num_q_heads, num_kv_heads,
+                        head_dim, max_seq_len, block_n, num_splits, advance_position, stream);
 }
 
 extern "C" int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_partial,

@@ -45,6 +45,8 @@ extern "C" const char* grout_status_string(int32_t status) {
         case GROUT_ERR_SPLITS: return "num_splits or block_n out of range";
         case GROUT_ERR_ARG: return "invalid scalar argument";
         case GROUT_ERR_GRAPH: return "invalid graph handle or capture state";
+        case GROUT_ERR_SCRATCH:
+            return "the call needs more than the library's static scratch (GROUT_NOALLOC_SCRATCH_BYTES)";
         default: break;
     }
     if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

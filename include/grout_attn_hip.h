@@ -51,7 +51,8 @@ enum {
     GROUT_ERR_GROUP = -7,         /* decode group outside [1, 16] */
     GROUT_ERR_SPLITS = -8,        /* num_splits or block_n out of range */
     GROUT_ERR_ARG = -9,           /* any other invalid scalar argument */
-    GROUT_ERR_GRAPH = -10         /* graph handle misuse */
+    GROUT_ERR_GRAPH = -10,        /* graph handle misuse */
+    GROUT_ERR_SCRATCH = -11       /* the static scratch of a *_noalloc entry point is too small */
 };
 
 /* Human-readable text for a status code (static storage). */
@@ -286,6 +287,30 @@ int32_t grout_attn_decode_fused(const uint16_t* qkv, const uint16_t* q_weight,
                                 int32_t block_n, int32_t num_splits, int32_t advance_position,
                                 grout_stream_t stream);
 int64_t grout_attn_decode_counter_bytes(int32_t num_kv_heads);
+
+/* The fused decode step without caller scratch.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as grout_attn_decode_fused minus
+ * att_partial, lse_partial and counters, which live in one static device
+ * array of GROUT_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends):
+ * 64 KiB of merge counters, then num_q_heads * num_splits LSEs (f32) and
+ * partial rows (256 B).  Calls needing more, or num_kv_heads above
+ * GROUT_NOALLOC_MAX_KV_HEADS, return GROUT_ERR_SCRATCH.  Nothing is
+ * allocated; the first call on a device looks up the array's address and
+ * clears its counters in stream order, and every launch leaves them zero.
+ * All calls on one GPU share the array: calls that overlap on one GPU (two
+ * streams, two threads) race. */
+#define GROUT_NOALLOC_SCRATCH_BYTES 4194304 /* 4 MiB */
+#define GROUT_NOALLOC_MAX_KV_HEADS 255
+int32_t grout_attn_decode_fused_noalloc(const uint16_t* qkv, const uint16_t* q_weight,
+                                        const uint16_t* k_weight, const float* inv_freq,
+                                        uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                        uint16_t* out, uint32_t* d_position, float eps,
+                                        uint16_t qk_scale_f16, int32_t num_q_heads,
+                                        int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t max_seq_len, int32_t block_n, int32_t num_splits,
+                                        int32_t advance_position, grout_stream_t stream);
 
 /* Bytes of att_partial (f16) and lse_partial (f32) for a split count, as
  * allocated at src/model.rs:2508-2525.  Returns < 0 on invalid arguments. */

@@ -49,6 +49,12 @@ pub const GROUT_ERR_GROUP: i32 = -7;
 pub const GROUT_ERR_SPLITS: i32 = -8;
 pub const GROUT_ERR_ARG: i32 = -9;
 pub const GROUT_ERR_GRAPH: i32 = -10;
+pub const GROUT_ERR_SCRATCH: i32 = -11;
+
+/// Static scratch of [`grout_attn_decode_fused_noalloc`] (per GPU) and the
+/// largest KV-head count it takes.
+pub const GROUT_NOALLOC_SCRATCH_BYTES: i32 = 4194304;
+pub const GROUT_NOALLOC_MAX_KV_HEADS: i32 = 255;
 
 /// Source element types of [`grout_cast_to_f16`] (`src/loader.rs:109-145`).
 pub const GROUT_DTYPE_F16: i32 = 0;
@@ -223,6 +229,15 @@ extern "C" {
         lse_partial: *mut f32, out: *mut u16, counters: *mut u32, d_position: *mut u32, eps: f32,
         qk_scale_f16: u16, num_q_heads: i32, num_kv_heads: i32, head_dim: i32, max_seq_len: i32,
         block_n: i32, num_splits: i32, advance_position: i32, stream: HipStream,
+    ) -> i32;
+    /// The fused step with its scratch in the library's static device
+    /// array; no counterpart in grout, for callers that cannot allocate.
+    pub fn grout_attn_decode_fused_noalloc(
+        qkv: *const u16, q_weight: *const u16, k_weight: *const u16, inv_freq: *const f32,
+        q_out: *mut u16, k_cache: *mut u16, v_cache: *mut u16, out: *mut u16,
+        d_position: *mut u32, eps: f32, qk_scale_f16: u16, num_q_heads: i32, num_kv_heads: i32,
+        head_dim: i32, max_seq_len: i32, block_n: i32, num_splits: i32, advance_position: i32,
+        stream: HipStream,
     ) -> i32;
     pub fn grout_attn_decode_counter_bytes(num_kv_heads: i32) -> i64;
     pub fn grout_attn_decode_partial_bytes(
