@@ -62,7 +62,7 @@ def header_functions() -> dict:
                          text):
         ret, name, args = m.group(1), m.group(2), " ".join(m.group(3).split())
         params = []
-        for a in args.split(","):
+        for a in ([] if args in ("", "void") else args.split(",")):
             a = a.strip()
             pm = re.match(r"(.*?)(\w+)$", a)
             params.append((pm.group(2), c_to_rust(pm.group(1).strip())))
