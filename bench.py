@@ -17,6 +17,10 @@ fp16 dense MFMA peak, and decode attention GB/s as a fraction of HBM peak.
             unsplit and split-K, then 64 graph-replayed decode steps), the
             Qwen3-4B decode at context 32768, c3's fused QK norm/RoPE/KV write,
             the decode-layer ops and the whole Qwen3-32B token step.
+  steady  = c3 once more at the end, after 200 further untimed launches
+            (prefill_c3_steady_state): from idle the GPU's power management
+            takes ~50 launches to settle, so the headline window (the
+            contract's warmup count) includes that transient.
 
 Kernel durations come from HIP events recorded on the launch stream, around a
 run of back-to-back launches divided by the count.  The CPU baseline is the
@@ -154,6 +158,17 @@ def bench_prefill(torch, ga, steps, warmup, gen):
     tflops = flops / (ms * 1e-3) / 1e12
     return dict(q=q, kc=kc, vc=vc, out=out, ms=ms, wall_ms=wall, tflops=tflops, flops=flops,
                 hq=hq, hkv=hkv, S=S)
+
+
+def bench_prefill_steady(torch, ga, pre, steps, sustain=200):
+    """The c3 prefill once the GPU's power management has settled: `sustain`
+    untimed launches on the c3 inputs, then `steps` launches timed as in
+    time_region.  From idle the first ~50 launches run slower (launches 5-25
+    average ~560 us against ~490 us after ~60 launches on the same box), so a
+    short warmup measures that transient rather than the kernel."""
+    fn = lambda: ga.attend_prefill(pre["q"], pre["kc"], pre["vc"], pre["out"], 0)  # noqa: E731
+    ms, _ = time_region(torch, fn, steps, sustain)
+    return dict(ms=ms, tflops=pre["flops"] / (ms * 1e-3) / 1e12, sustain=sustain)
 
 
 def bench_prefill_split(torch, ga, pre, steps, num_splits=4, block_m=128, block_n=64):
@@ -957,6 +972,11 @@ def main(argv=None) -> int:
     log(f"token step c4 ({ts['layers']} layers, ctx {ts['ctx']}): {ts['ms']:.3f} ms/token, "
         f"{ts['tokens_per_s']:.1f} tok/s, {ts['gbs']:.0f} GB/s")
 
+    log("prefill c3 in the settled power state ...")
+    steady = bench_prefill_steady(torch, ga, pre, args.steps)
+    log(f"prefill c3 after {steady['sustain']} untimed launches: {steady['ms']:.3f} ms/launch, "
+        f"{steady['tflops']:.1f} TFLOP/s (headline window: {pre['ms']:.3f} ms)")
+
     cpu = None
     if not args.no_cpu_baseline:
         threads, visible = host_threads()
@@ -1104,6 +1124,14 @@ def main(argv=None) -> int:
             "bytes_per_token": ts["bytes"], "GB/s": round(ts["gbs"], 1),
             "frac_of_hbm_peak": round(ts["gbs"] / PEAK_HBM_GBS, 4),
             "num_splits": ts["num_splits"], "steps": ts["steps"]},
+        "prefill_c3_steady_state": {
+            "note": "the same c3 launches after the bench's other legs and "
+                    f"{steady['sustain']} more untimed launches, once the GPU's power "
+                    "management has settled; the headline value keeps the contract's "
+                    "warmup count",
+            "ms_per_step": round(steady["ms"], 4), "TFLOP/s": round(steady["tflops"], 2),
+            "frac_of_fp16_peak": round(steady["tflops"] / PEAK_TFLOPS_F16, 4),
+            "untimed_launches_before": steady["sustain"], "steps": args.steps},
         "qk_norm_rope_c3": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                             "frac_of_hbm_peak": round(nrm["gbs"] / PEAK_HBM_GBS, 4)},
         "kv_cache_update_c3": {"us": round(kvu["ms"] * 1e3, 2), "GB/s": round(kvu["gbs"], 1),
