@@ -151,13 +151,21 @@ def bench_prefill(torch, ga, steps, warmup, gen):
     kc = torch.randn((hkv, S, D), device="cuda", generator=gen, dtype=torch.float32).half()
     vc = torch.randn((hkv, S, D), device="cuda", generator=gen, dtype=torch.float32).half()
     out = torch.empty_like(q)
-    fn = lambda: ga.attend_prefill(q, kc, vc, out, 0)  # noqa: E731
+    counters = ga.prefill_sched_counters()
+    fn = lambda: ga.attend_prefill(q, kc, vc, out, 0, sched_counters=counters)  # noqa: E731
     ms, wall = time_region(torch, fn, steps, warmup)
     assert torch.isfinite(out).all().item(), "non-finite prefill output"
+    # The static grid (grout_attn_prefill) right after, same inputs: its output
+    # is bit-identical, only the schedule differs.
+    out_st = torch.empty_like(q)
+    sfn = lambda: ga.attend_prefill(q, kc, vc, out_st, 0)  # noqa: E731
+    static_ms, _ = time_region(torch, sfn, steps, 2)
+    assert torch.equal(out_st.view(torch.int16), out.view(torch.int16)), "schedules disagree"
+    del out_st
     flops = prefill_flops(hq, S)
     tflops = flops / (ms * 1e-3) / 1e12
     return dict(q=q, kc=kc, vc=vc, out=out, ms=ms, wall_ms=wall, tflops=tflops, flops=flops,
-                hq=hq, hkv=hkv, S=S)
+                hq=hq, hkv=hkv, S=S, static_ms=static_ms, counters=counters)
 
 
 def bench_prefill_steady(torch, ga, pre, steps, sustain=200):
@@ -166,7 +174,8 @@ def bench_prefill_steady(torch, ga, pre, steps, sustain=200):
     time_region.  From idle the first ~50 launches run slower (launches 5-25
     average ~560 us against ~490 us after ~60 launches on the same box), so a
     short warmup measures that transient rather than the kernel."""
-    fn = lambda: ga.attend_prefill(pre["q"], pre["kc"], pre["vc"], pre["out"], 0)  # noqa: E731
+    fn = lambda: ga.attend_prefill(pre["q"], pre["kc"], pre["vc"], pre["out"], 0,  # noqa: E731
+                                   sched_counters=pre["counters"])
     ms, _ = time_region(torch, fn, steps, sustain)
     return dict(ms=ms, tflops=pre["flops"] / (ms * 1e-3) / 1e12, sustain=sustain)
 
@@ -577,9 +586,14 @@ def bench_c5(torch, ga, gen, steps: int = 5, warmup: int = 3, decode_steps: int 
     c5 = make_c5_inputs(torch, gen)
     q, kc, vc, hq, hkv, S = c5["q"], c5["kc"], c5["vc"], c5["hq"], c5["hkv"], c5["S"]
     out = torch.empty_like(q)
-    fn = lambda: ga.attend_prefill(q, kc, vc, out, 0)  # noqa: E731
+    counters = ga.prefill_sched_counters()
+    fn = lambda: ga.attend_prefill(q, kc, vc, out, 0, sched_counters=counters)  # noqa: E731
     ms, _ = time_region(torch, fn, steps, warmup)
     assert torch.isfinite(out).all().item(), "non-finite c5 prefill output"
+    out_st = torch.empty_like(q)
+    static_ms, _ = time_region(torch, lambda: ga.attend_prefill(q, kc, vc, out_st, 0), steps, 1)
+    assert torch.equal(out_st.view(torch.int16), out.view(torch.int16)), "c5 schedules disagree"
+    del out_st
     flops = prefill_flops(hq, S)
     # Split-K prefill (fmha_prefill_gqa_lpt_split + merge) on the same inputs.
     ns, bm, bn = split
@@ -625,7 +639,8 @@ def bench_c5(torch, ga, gen, steps: int = 5, warmup: int = 3, decode_steps: int 
     finally:
         runner.close()
     dec_bytes = sum(decode_bytes(hq, hkv, S + i + 1) for i in range(decode_steps))
-    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, flops=flops, split_ms=split_ms,
+    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, flops=flops, static_ms=static_ms,
+                split_ms=split_ms,
                 merge_ms=merge_ms, split_tflops=flops / ((split_ms + merge_ms) * 1e-3) / 1e12,
                 split=split, split_max_diff=split_diff, decode_steps=decode_steps,
                 decode_us=dec_us, decode_bytes=dec_bytes,
@@ -861,7 +876,7 @@ def main(argv=None) -> int:
     if args.only != "all":
         if args.only == "prefill":
             pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
-            log(f"prefill c3: {pre['ms']:.3f} ms/launch, {pre['tflops']:.1f} TFLOP/s")
+            log(f"prefill c3: {pre['ms']:.3f} ms/launch, {pre['tflops']:.1f} TFLOP/s (static grid {pre['static_ms']:.3f} ms)")
         elif args.only == "norm":
             nrm = bench_norm(torch, ga, args.steps, args.warmup, gen)
             log(f"norm c3: {nrm['ms'] * 1e3:.1f} us, {nrm['gbs']:.0f} GB/s")
@@ -916,7 +931,7 @@ def main(argv=None) -> int:
 
     log("prefill c3 ...")
     pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
-    log(f"prefill c3: {pre['ms']:.3f} ms/launch, {pre['tflops']:.1f} TFLOP/s")
+    log(f"prefill c3: {pre['ms']:.3f} ms/launch, {pre['tflops']:.1f} TFLOP/s (static grid {pre['static_ms']:.3f} ms)")
     log("prefill split-K c3 ...")
     psp = bench_prefill_split(torch, ga, pre, args.steps)
     log(f"prefill split-K c3: split {psp['ms'] * 1e3:.1f} us + merge {psp['merge_ms'] * 1e3:.1f} us, "
@@ -1014,7 +1029,10 @@ def main(argv=None) -> int:
         "config": {"workload": "c3: Qwen3-4B causal prefill attention, batch 1, S=8192, "
                                "32 Q / 8 KV heads, head_dim 128, f16 (fp32 accumulation)",
                    "seq_len": pre["S"], "num_q_heads": pre["hq"], "num_kv_heads": pre["hkv"],
-                   "head_dim": D, "flops_per_step": pre["flops"]},
+                   "head_dim": D, "flops_per_step": pre["flops"],
+                   "entry_point": "grout_attn_prefill_sched (dynamic per-XCD schedule)",
+                   "static_grid_ms_per_step": round(pre["static_ms"], 4),
+                   "static_grid_TFLOP/s": round(pre["flops"] / (pre["static_ms"] * 1e-3) / 1e12, 2)},
         "roofline": rl("mfma", pre["tflops"], PEAK_TFLOPS_F16, "TFLOP/s",
                        traffic=round(PMC_TRAFFIC_BYTES["attn_prefill_c3"])),
         "cpu_baseline": cpu_entry("c3"),
@@ -1070,6 +1088,7 @@ def main(argv=None) -> int:
             "workload": "Qwen3-32B causal prefill, S=32768, 64 Q / 8 KV heads, 1% of K rows x8, "
                         f"then {c5['decode_steps']} graph-replayed decode steps on the same cache",
             "prefill_ms": round(c5["ms"], 3),
+            "prefill_static_grid_ms": round(c5["static_ms"], 3),
             "roofline": rl("mfma", c5["tflops"], PEAK_TFLOPS_F16, "TFLOP/s"),
             "prefill_flops": c5["flops"], "outlier_k_rows": c5["n_outlier_rows"],
             "split_k": {"num_splits": c5["split"][0], "block_m": c5["split"][1],

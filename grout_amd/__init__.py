@@ -200,11 +200,14 @@ def qk_norm_rope_kv_decode(qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_
 
 
 def attend_prefill(q, k_cache, v_cache, out, position_start: int,
-                   qk_scale: float | None = None, kv_len: int | None = None):
+                   qk_scale: float | None = None, kv_len: int | None = None,
+                   sched_counters=None):
     """attend_seq_arc_into_ctx_with_position with a host position (src/model.rs:5556-5834).
 
     kv_len defaults to position_start + q_len (:5638); qk_scale to 1/sqrt(D) in
-    f32 (:5601)."""
+    f32 (:5601).  With `sched_counters` (prefill_sched_counters()) the launch
+    uses the dynamic per-XCD schedule (grout_attn_prefill_sched); the result
+    is bit-identical to the static grid's."""
     _ensure(q.dim() == 3, f"q must be rank 3 [seqlen, heads, head_dim], got {list(q.shape)}")
     q_len, Hq, D = q.shape
     Hkv, MS, _ = k_cache.shape
@@ -216,10 +219,27 @@ def attend_prefill(q, k_cache, v_cache, out, position_start: int,
         kv_len = position_start + q_len
     for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out")):
         _f16(t, n)
-    _check(lib().grout_attn_prefill(
-        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), float(qk_scale), Hq, Hkv, D, q_len,
-        int(kv_len), int(position_start), MS, _stream()), "attn_prefill")
+    args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), float(qk_scale), Hq, Hkv, D, q_len,
+            int(kv_len), int(position_start), MS)
+    if sched_counters is None:
+        _check(lib().grout_attn_prefill(*args, _stream()), "attn_prefill")
+    else:
+        _ensure(sched_counters.is_cuda and sched_counters.is_contiguous(),
+                "sched_counters must be a contiguous device tensor")
+        _ensure(sched_counters.numel() * sched_counters.element_size()
+                >= lib().grout_attn_prefill_sched_counter_bytes(),
+                "sched_counters is smaller than grout_attn_prefill_sched_counter_bytes()")
+        _check(lib().grout_attn_prefill_sched(*args, _ptr(sched_counters), _stream()),
+               "attn_prefill_sched")
     return out
+
+
+def prefill_sched_counters(device="cuda"):
+    """Zeroed counters for attend_prefill(..., sched_counters=...): every launch
+    leaves them zero again.  Launches that overlap on one buffer race."""
+    torch = _torch()
+    n = lib().grout_attn_prefill_sched_counter_bytes() // 4
+    return torch.zeros((n,), dtype=torch.int32, device=device)
 
 
 def prefill_split_scratch(num_q_heads: int, q_len: int, block_m: int, group: int,

@@ -78,6 +78,8 @@ SIGNATURES = {
     "grout_qk_norm_rope_kv_decode": (
         c_i32, [c_vp] * 8 + [c_f32] + [c_i32] * 4 + [c_vp]),
     "grout_attn_prefill": (c_i32, [c_vp] * 4 + [c_f32] + [c_i32] * 7 + [c_vp]),
+    "grout_attn_prefill_sched": (c_i32, [c_vp] * 4 + [c_f32] + [c_i32] * 7 + [c_vp, c_vp]),
+    "grout_attn_prefill_sched_counter_bytes": (c_i64, []),
     "grout_attn_prefill_split": (c_i32, [c_vp] * 5 + [c_f32] + [c_i32] * 11 + [c_vp]),
     "grout_attn_prefill_split_merge": (c_i32, [c_vp] * 3 + [c_i32] * 6 + [c_vp]),
     "grout_attn_prefill_split_partial_bytes": (c_i64, [c_i32] * 6),

@@ -87,7 +87,22 @@ struct PrefillArgs {
     int block_n;            // BN: keys per split-range tile
     int split_group;        // GROUP: q heads per logical tile
     int num_splits;
+    // Dynamic schedule only (kDyn): per-queue claim counters (kPfQueues words,
+    // then the exit counter, kPfSchedStride u32 apart, zero on entry and exit),
+    // the number of persistent workgroups and the KV-head count.
+    uint32_t* sched;
+    int n_wg;
+    int num_kv_heads;
 };
+
+// Dynamic schedule: queue q holds the tasks (workgroup-sized units, as the
+// static grid's blocks) of KV heads h = q (mod kPfQueues), heaviest first.
+// A persistent workgroup claims from the queue of the XCD it runs on, so a
+// head's K/V stay in that XCD's L2, and takes from the fullest other queue
+// once its own is empty, so XCDs that run faster take over the tail.
+constexpr int kPfQueues = 8;
+constexpr int kPfSchedStride = 64;  // u32: one 256-byte line per counter
+constexpr int kPfClaimAttempts = 64;
 
 // Asynchronous 16-byte HBM -> LDS copy (global_load_lds_dwordx4, scalar base
 // + 32-bit per-lane byte offset): lane l's 16 bytes land at LDS byte
@@ -134,8 +149,12 @@ constexpr int kPfRows = 32;
 // its split's range, computed from the reference's q block of its rows
 // (block_m is a multiple of 32, so a wavefront's rows lie in one block), and
 // stores a normalised partial and its log2 LSE instead of the output.
-template <bool kSplit>
+// kDyn: persistent workgroups that claim tasks from the per-XCD queues above
+// instead of taking one task from blockIdx; each task runs exactly as in the
+// static grid, so the output is bit-identical.
+template <bool kSplit, bool kDyn>
 __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(PrefillArgs a) {
+    static_assert(!(kSplit && kDyn), "the split-K form keeps the static grid");
     constexpr int kDmaPerWave = 16 / kPfWaves;  // K blocks (and V blocks) per wavefront
     __shared__ __attribute__((aligned(1024))) unsigned char pf_lds[kPfStages * kPfStageBytes];
 
@@ -151,7 +170,77 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     // within a head the latest (heaviest) position tiles come first.
     const int nb = gridDim.x;
     const int b = blockIdx.x;
-    const int T = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    int T = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+
+    // Dynamic schedule state (wave 0 claims; the task goes to all waves
+    // through LDS).  The claim on the own queue is issued one task ahead, after
+    // the previous task's loop, so its round trip overlaps that epilogue.
+    __shared__ int s_task;
+    int my_q = 0, nhq_own = 0, nq_own = 0;
+    bool own_live = false;
+    uint32_t pre_j = 0xffffffffu;  // prefetched own-queue ticket (wave 0, lane 0)
+    if constexpr (kDyn) {
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        my_q = static_cast<int>(xcc % kPfQueues);
+        nhq_own = a.num_kv_heads > my_q ? (a.num_kv_heads - my_q + kPfQueues - 1) / kPfQueues : 0;
+        nq_own = nhq_own * a.blocks_per_head;
+        own_live = nq_own > 0;
+        if (wave == 0 && lane == 0 && own_live)
+            pre_j = __hip_atomic_fetch_add(a.sched + my_q * kPfSchedStride, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Task j of queue q: KV head q + kPfQueues*(j % nhq), block j / nhq.
+    auto queue_task = [&](int q, int nhq, int j) {
+        return (q + kPfQueues * (j % nhq)) * a.blocks_per_head + j / nhq;
+    };
+
+    for (;;) {
+    if constexpr (kDyn) {
+        if (wave == 0) {
+            int task = -1;
+            const int j0 = static_cast<int>(__shfl(pre_j, 0));
+            if (own_live && j0 >= 0 && j0 < nq_own) {
+                task = queue_task(my_q, nhq_own, j0);
+            } else {
+                own_live = false;
+            }
+            // Own queue empty: claim from the queue with the most tasks left;
+            // leave once every queue is empty.
+            for (int attempt = 0; attempt < kPfClaimAttempts && task < 0; ++attempt) {
+                int rem = 0;
+                if (lane < kPfQueues) {
+                    const int nhq = a.num_kv_heads > lane ? (a.num_kv_heads - lane + kPfQueues - 1) / kPfQueues : 0;
+                    const uint32_t nq = static_cast<uint32_t>(nhq * a.blocks_per_head);
+                    const uint32_t c = __hip_atomic_load(a.sched + lane * kPfSchedStride, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                    rem = static_cast<int>(nq - min(c, nq));
+                }
+                int best = -1, best_rem = 0;
+#pragma unroll
+                for (int q = 0; q < kPfQueues; ++q) {
+                    const int r = __shfl(rem, q);
+                    if (r > best_rem) {
+                        best_rem = r;
+                        best = q;
+                    }
+                }
+                if (best < 0) break;
+                uint32_t j = 0;
+                if (lane == 0)
+                    j = __hip_atomic_fetch_add(a.sched + best * kPfSchedStride, 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                j = __shfl(j, 0);
+                const int nhq = (a.num_kv_heads - best + kPfQueues - 1) / kPfQueues;
+                if (j < static_cast<uint32_t>(nhq * a.blocks_per_head))
+                    task = queue_task(best, nhq, static_cast<int>(j));
+            }
+            if (lane == 0) s_task = task;
+        }
+        pf_barrier();  // also: every wavefront is past the previous task's LDS reads
+        T = s_task;
+        if (T < 0) break;
+    }
     const int kvh = T / a.blocks_per_head;
     const int rblk = T % a.blocks_per_head;
     const int u = rblk * kPfWaves + wave;
@@ -451,7 +540,12 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
         }
     }
 
-    if (!task_ok) return;
+    if constexpr (kDyn) {
+        if (wave == 0 && lane == 0 && own_live)
+            pre_j = __hip_atomic_fetch_add(a.sched + my_q * kPfSchedStride, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (task_ok) {
     // out[row][d] with d = 32db + 8(r/4) + 4hl + r%4.
     const int row = row0 + l32;
     const float lt = l_run + swap_halves(l_run);
@@ -480,9 +574,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
                 *reinterpret_cast<half4_t*>(prow_p + 32 * db + 8 * i + 4 * hl) = h;
             }
         if (hl == 0) a.lse_partial[prow] = m_run + log2f(l_safe);
-        return;
-    }
-    if (row < a.q_len) {
+    } else if (row < a.q_len) {
         uint16_t* orow = a.out + (static_cast<int64_t>(row) * a.num_q_heads + qh) * kHeadDim;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
@@ -494,6 +586,23 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
                 *reinterpret_cast<half4_t*>(orow + 32 * db + 8 * i + 4 * hl) = h;
             }
     }
+    }  // task_ok
+    if constexpr (!kDyn) break;
+    }  // task loop
+
+    if constexpr (kDyn) {
+        // The last workgroup to leave clears the counters for the next launch:
+        // every other one has stopped claiming before its exit increment.
+        if (tid == 0) {
+            const uint32_t done = __hip_atomic_fetch_add(a.sched + kPfQueues * kPfSchedStride, 1u,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (done + 1 == static_cast<uint32_t>(a.n_wg)) {
+                for (int q = 0; q <= kPfQueues; ++q)
+                    __hip_atomic_store(a.sched + q * kPfSchedStride, 0u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
 }
 
 static int32_t launch_prefill(PrefillArgs a, int num_kv_heads, hipStream_t stream) {
@@ -502,7 +611,30 @@ static int32_t launch_prefill(PrefillArgs a, int num_kv_heads, hipStream_t strea
     a.blocks_per_head = (a.tasks_per_head + kPfWaves - 1) / kPfWaves;
     const int64_t blocks = static_cast<int64_t>(a.blocks_per_head) * num_kv_heads;
     if (blocks > 0x7fffffff) return GROUT_ERR_KV_LEN;
-    hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((attn_prefill_kernel<false, false>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kPfWaves * kWave), 0, stream, a);
+    return launch_status();
+}
+
+// Dynamic schedule: one persistent workgroup per CU (the kernel's LDS allows
+// one) when the static grid would run more than two rounds of workgroups;
+// smaller grids keep the static launch, which then leaves the counters alone.
+static int32_t launch_prefill_sched(PrefillArgs a, int num_kv_heads, uint32_t* sched,
+                                    hipStream_t stream) {
+    a.n_pos_tiles = (a.q_len + kPfRows - 1) / kPfRows;
+    a.tasks_per_head = a.n_pos_tiles * a.group;
+    a.blocks_per_head = (a.tasks_per_head + kPfWaves - 1) / kPfWaves;
+    const int64_t blocks = static_cast<int64_t>(a.blocks_per_head) * num_kv_heads;
+    if (blocks > 0x7fffffff) return GROUT_ERR_KV_LEN;
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return static_cast<int32_t>(e);
+    if (cus <= 0 || blocks <= 2 * static_cast<int64_t>(cus)) return launch_prefill(a, num_kv_heads, stream);
+    a.sched = sched;
+    a.n_wg = cus;
+    a.num_kv_heads = num_kv_heads;
+    hipLaunchKernelGGL((attn_prefill_kernel<false, true>), dim3(static_cast<unsigned>(cus)),
                        dim3(kPfWaves * kWave), 0, stream, a);
     return launch_status();
 }
@@ -553,7 +685,7 @@ static int32_t launch_prefill_split(PrefillArgs a, int num_kv_heads, hipStream_t
     a.n_pos_tiles = static_cast<int>(pos_tiles);
     a.tasks_per_head = static_cast<int>(tasks);
     a.blocks_per_head = static_cast<int>(bph);
-    hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3(static_cast<unsigned>(blocks), a.num_splits),
+    hipLaunchKernelGGL((attn_prefill_kernel<true, false>), dim3(static_cast<unsigned>(blocks), a.num_splits),
                        dim3(kPfWaves * kWave), 0, stream, a);
     return launch_status();
 }
@@ -573,13 +705,14 @@ static int64_t prefill_split_rows(int32_t num_q_heads, int32_t q_len, int32_t bl
 
 using namespace grout;
 
-extern "C" int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
-                                      const uint16_t* v_cache, uint16_t* out, float qk_scale,
-                                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                                      int32_t q_len, int32_t kv_len, int32_t query_start,
-                                      int32_t max_seq_len, grout_stream_t stream) {
-    // Mirrors the ensure!s of attend_seq_arc_into_ctx_with_position
-    // (src/model.rs:5564-5637) on sizes.
+// Shared by both prefill entry points: the ensure!s of
+// attend_seq_arc_into_ctx_with_position (src/model.rs:5564-5637) on sizes, then
+// the static grid (sched == nullptr) or the dynamic schedule.
+static int32_t prefill_entry(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                             uint16_t* out, float qk_scale, int32_t num_q_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t q_len, int32_t kv_len,
+                             int32_t query_start, int32_t max_seq_len, uint32_t* sched,
+                             grout_stream_t stream) {
     GROUT_REQUIRE_PTR(q);
     GROUT_REQUIRE_PTR(k_cache);
     GROUT_REQUIRE_PTR(v_cache);
@@ -593,7 +726,7 @@ extern "C" int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache
     GROUT_REQUIRE(qk_scale > 0.0f && qk_scale < 1.0e30f, GROUT_ERR_ARG);
     if (q_len == 0) return GROUT_OK;
 
-    PrefillArgs a;
+    PrefillArgs a = {};
     a.q = q;
     a.k_cache = k_cache;
     a.v_cache = v_cache;
@@ -606,7 +739,34 @@ extern "C" int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache
     a.kv_len = kv_len;
     a.query_start = query_start;
     a.max_seq_len = max_seq_len;
-    return launch_prefill(a, num_kv_heads, to_hip(stream));
+    if (sched == nullptr) return launch_prefill(a, num_kv_heads, to_hip(stream));
+    return launch_prefill_sched(a, num_kv_heads, sched, to_hip(stream));
+}
+
+extern "C" int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
+                                      const uint16_t* v_cache, uint16_t* out, float qk_scale,
+                                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                      int32_t q_len, int32_t kv_len, int32_t query_start,
+                                      int32_t max_seq_len, grout_stream_t stream) {
+    return prefill_entry(q, k_cache, v_cache, out, qk_scale, num_q_heads, num_kv_heads, head_dim,
+                         q_len, kv_len, query_start, max_seq_len, nullptr, stream);
+}
+
+extern "C" int32_t grout_attn_prefill_sched(const uint16_t* q, const uint16_t* k_cache,
+                                            const uint16_t* v_cache, uint16_t* out,
+                                            float qk_scale, int32_t num_q_heads,
+                                            int32_t num_kv_heads, int32_t head_dim, int32_t q_len,
+                                            int32_t kv_len, int32_t query_start,
+                                            int32_t max_seq_len, uint32_t* sched_counters,
+                                            grout_stream_t stream) {
+    GROUT_REQUIRE(sched_counters != nullptr, GROUT_ERR_NULL_POINTER);
+    GROUT_REQUIRE((reinterpret_cast<uintptr_t>(sched_counters) & 3u) == 0, GROUT_ERR_ALIGNMENT);
+    return prefill_entry(q, k_cache, v_cache, out, qk_scale, num_q_heads, num_kv_heads, head_dim,
+                         q_len, kv_len, query_start, max_seq_len, sched_counters, stream);
+}
+
+extern "C" int64_t grout_attn_prefill_sched_counter_bytes(void) {
+    return static_cast<int64_t>(kPfQueues + 1) * kPfSchedStride * 4;
 }
 
 extern "C" int32_t grout_attn_prefill_split(const uint16_t* q, const uint16_t* k_cache,

@@ -147,6 +147,24 @@ int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uin
                            int32_t kv_len, int32_t query_start, int32_t max_seq_len,
                            grout_stream_t stream);
 
+/* Same computation, scheduled dynamically: one persistent workgroup per CU
+ * claims workgroup-sized tasks from per-XCD queues (the KV heads
+ * h = q (mod 8) in queue q, heaviest first), its own XCD's queue first, then
+ * the fullest other queue, so XCDs that run faster take over the tail (the
+ * reference's LPT order, fmha_prefill_gqa_lpt src/kernels.rs:1513-1862, made
+ * dynamic).  Output bit-identical to grout_attn_prefill.  Grids of at most two
+ * rounds of workgroups use the static launch and leave the counters alone.
+ *   sched_counters: grout_attn_prefill_sched_counter_bytes() bytes, 4-byte
+ *   aligned, zero before the first call; every call leaves them zero.
+ * Calls that overlap on one set of counters race. */
+int32_t grout_attn_prefill_sched(const uint16_t* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, uint16_t* out, float qk_scale,
+                                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                 int32_t q_len, int32_t kv_len, int32_t query_start,
+                                 int32_t max_seq_len, uint32_t* sched_counters,
+                                 grout_stream_t stream);
+int64_t grout_attn_prefill_sched_counter_bytes(void);
+
 /* --------------------------------------------------- split-K prefill (A8) */
 /* Replaces fmha_prefill_gqa_lpt_split (src/kernels.rs:1872-2142), launched by
  * the attention microbench (benchmarks/src/bin/attention_microbench.rs:418-469)

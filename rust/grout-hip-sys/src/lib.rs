@@ -176,6 +176,14 @@ extern "C" {
         num_q_heads: i32, num_kv_heads: i32, head_dim: i32, q_len: i32, kv_len: i32,
         query_start: i32, max_seq_len: i32, stream: HipStream,
     ) -> i32;
+    /// The same prefill with a dynamic per-XCD schedule; `sched_counters` is
+    /// [`grout_attn_prefill_sched_counter_bytes`] zeroed bytes kept by the engine.
+    pub fn grout_attn_prefill_sched(
+        q: *const u16, k_cache: *const u16, v_cache: *const u16, out: *mut u16, qk_scale: f32,
+        num_q_heads: i32, num_kv_heads: i32, head_dim: i32, q_len: i32, kv_len: i32,
+        query_start: i32, max_seq_len: i32, sched_counters: *mut u32, stream: HipStream,
+    ) -> i32;
+    pub fn grout_attn_prefill_sched_counter_bytes() -> i64;
     pub fn grout_attn_prefill_split(
         q: *const u16, k_cache: *const u16, v_cache: *const u16, att_partial: *mut u16,
         lse_partial: *mut f32, qk_scale: f32, num_q_heads: i32, num_kv_heads: i32, head_dim: i32,

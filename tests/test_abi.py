@@ -110,6 +110,30 @@ def test_prefill_checks(L):
     assert call(ql=0) == 0
 
 
+def test_prefill_sched_checks(L):
+    """grout_attn_prefill_sched: its counters are checked first, then the same
+    argument checks as grout_attn_prefill (one shared validation path)."""
+    f = L.grout_attn_prefill_sched
+    ok = dict(q=A, k=A, v=A, o=A, sc=0.088, hq=4, hkv=2, D=128, ql=8, kv=8, qs=0, MS=16, c=A)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return f(a["q"], a["k"], a["v"], a["o"], a["sc"], a["hq"], a["hkv"], a["D"], a["ql"],
+                 a["kv"], a["qs"], a["MS"], a["c"], S)
+
+    assert call(c=0) == -1
+    assert call(c=U) == -2
+    assert call(o=0) == -1
+    assert call(q=U) == -2
+    assert call(D=256) == -3
+    assert call(hq=5) == -4
+    assert call(kv=17) == -6
+    assert call(sc=0.0) == -9
+    assert call(ql=0) == 0
+    # 8 queue counters and the exit counter, one 256-byte line each.
+    assert L.grout_attn_prefill_sched_counter_bytes() == 9 * 256
+
+
 def test_prefill_split_checks(L):
     f = L.grout_attn_prefill_split
     ok = dict(q=A, k=A, v=A, att=A, lse=A, sc=0.088, hq=8, hkv=2, D=128, ql=40, kv=40, qs=0,
