@@ -59,7 +59,9 @@ PEAK_HBM_GBS = 8000.0      # HBM3E
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0), the
 # scales read off a 1 GiB copy; the runs and figures are in profiles/*.txt.
 PMC_TRAFFIC_BYTES = {
-    "attn_prefill_c3": (71767.0 * 2.0 + 65536.0) * 1024,
+    # grout_attn_prefill_sched (the headline's entry point); the static grid read
+    # 71989.8 and wrote 65539.6 KiB on the same run.
+    "attn_prefill_c3": (72109.6 * 2.0 + 66223.4) * 1024,
     "attn_decode_fused_c4": (65976.8 * 2.0 + 572.3) * 1024,
 }
 D = 128
