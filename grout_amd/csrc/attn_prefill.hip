@@ -179,6 +179,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     int my_q = 0, nhq_own = 0, nq_own = 0;
     bool own_live = false;
     uint32_t pre_j = 0xffffffffu;  // prefetched own-queue ticket (wave 0, lane 0)
+    int pre_ticket = -1;           // the same, read back (wave 0, uniform); -1: none
     if constexpr (kDyn) {
         uint32_t xcc;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
@@ -189,6 +190,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
         if (wave == 0 && lane == 0 && own_live)
             pre_j = __hip_atomic_fetch_add(a.sched + my_q * kPfSchedStride, 1u, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
+        if (wave == 0 && own_live) pre_ticket = static_cast<int>(__shfl(pre_j, 0));
     }
     // Task j of queue q: KV head q + kPfQueues*(j % nhq), block j / nhq.
     auto queue_task = [&](int q, int nhq, int j) {
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     if constexpr (kDyn) {
         if (wave == 0) {
             int task = -1;
-            const int j0 = static_cast<int>(__shfl(pre_j, 0));
+            const int j0 = pre_ticket;
             if (own_live && j0 >= 0 && j0 < nq_own) {
                 task = queue_task(my_q, nhq_own, j0);
             } else {
@@ -574,18 +576,32 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
                 *reinterpret_cast<half4_t*>(prow_p + 32 * db + 8 * i + 4 * hl) = h;
             }
         if (hl == 0) a.lse_partial[prow] = m_run + log2f(l_safe);
-    } else if (row < a.q_len) {
-        uint16_t* orow = a.out + (static_cast<int64_t>(row) * a.num_q_heads + qh) * kHeadDim;
+    } else {
+        half4_t hv[16];
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                half4_t h;
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) h[e] = static_cast<half_t>(o[db][4 * i + e] / l_safe);
-                *reinterpret_cast<half4_t*>(orow + 32 * db + 8 * i + 4 * hl) = h;
-            }
+                for (int e = 0; e < 4; ++e) hv[4 * db + i][e] = static_cast<half_t>(o[db][4 * i + e] / l_safe);
+        if constexpr (kDyn) {
+            // The ticket claimed after the loop is read back before the
+            // stores go out: vmcnt also counts stores, so reading it after
+            // them would wait for the stores as well.
+            if (wave == 0) pre_ticket = own_live ? static_cast<int>(__shfl(pre_j, 0)) : -1;
+            asm volatile("" ::: "memory");
+        }
+        if (row < a.q_len) {
+            uint16_t* orow = a.out + (static_cast<int64_t>(row) * a.num_q_heads + qh) * kHeadDim;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    *reinterpret_cast<half4_t*>(orow + 32 * db + 8 * i + 4 * hl) = hv[4 * db + i];
+        }
     }
+    } else if constexpr (kDyn) {
+        if (wave == 0) pre_ticket = own_live ? static_cast<int>(__shfl(pre_j, 0)) : -1;
     }  // task_ok
     if constexpr (!kDyn) break;
     }  // task loop
