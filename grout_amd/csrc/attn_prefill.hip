@@ -87,20 +87,28 @@ struct PrefillArgs {
     int block_n;            // BN: keys per split-range tile
     int split_group;        // GROUP: q heads per logical tile
     int num_splits;
-    // Dynamic schedule only (kDyn): per-queue claim counters (kPfQueues words,
-    // then the exit counter, kPfSchedStride u32 apart, zero on entry and exit),
-    // the number of persistent workgroups and the KV-head count.
+    // Dynamic schedule only (kDyn): claim counters (kPfQueues XCD queues, the
+    // shared pool, the exit counter; kPfSchedStride u32 apart, zero on entry
+    // and exit), the number of persistent workgroups, the KV-head count and
+    // the first block (per head) that goes to the shared pool.
     uint32_t* sched;
     int n_wg;
     int num_kv_heads;
+    int pool_block0;
 };
 
-// Dynamic schedule: queue q holds the tasks (workgroup-sized units, as the
-// static grid's blocks) of KV heads h = q (mod kPfQueues), heaviest first.
-// A persistent workgroup claims from the queue of the XCD it runs on, so a
-// head's K/V stay in that XCD's L2, and takes from the fullest other queue
-// once its own is empty, so XCDs that run faster take over the tail.
+// Dynamic schedule.  A task is a workgroup-sized unit (one block of the static
+// grid).  Blocks [0, pool_block0) of the KV heads h = q (mod kPfQueues) form
+// XCD queue q, heaviest first; the lighter blocks [pool_block0, blocks_per_head)
+// of every head form one shared pool, heaviest first with the heads
+// interleaved.  A persistent workgroup claims from the queue of the XCD it
+// runs on (a head's K/V stay in that XCD's L2), then from the fullest other
+// XCD queue, then from the pool: XCDs that run faster take over the slower
+// ones' heavy blocks, and the last tasks anywhere are the lightest ones.
 constexpr int kPfQueues = 8;
+constexpr int kPfPool = kPfQueues;          // counter index of the shared pool
+constexpr int kPfExit = kPfQueues + 1;      // counter index of the exit counter
+constexpr int kPfSchedCounters = kPfQueues + 2;
 constexpr int kPfSchedStride = 64;  // u32: one 256-byte line per counter
 constexpr int kPfClaimAttempts = 64;
 
@@ -185,17 +193,19 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
         my_q = static_cast<int>(xcc % kPfQueues);
         nhq_own = a.num_kv_heads > my_q ? (a.num_kv_heads - my_q + kPfQueues - 1) / kPfQueues : 0;
-        nq_own = nhq_own * a.blocks_per_head;
+        nq_own = nhq_own * a.pool_block0;
         own_live = nq_own > 0;
         if (wave == 0 && lane == 0 && own_live)
             pre_j = __hip_atomic_fetch_add(a.sched + my_q * kPfSchedStride, 1u, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
         if (wave == 0 && own_live) pre_ticket = static_cast<int>(__shfl(pre_j, 0));
     }
-    // Task j of queue q: KV head q + kPfQueues*(j % nhq), block j / nhq.
+    // Task j of XCD queue q: KV head q + kPfQueues*(j % nhq), block j / nhq;
+    // task j of the pool: KV head j % Hkv, block pool_block0 + j / Hkv.
     auto queue_task = [&](int q, int nhq, int j) {
         return (q + kPfQueues * (j % nhq)) * a.blocks_per_head + j / nhq;
     };
+    const int n_pool = a.num_kv_heads * (a.blocks_per_head - a.pool_block0);
 
     for (;;) {
     if constexpr (kDyn) {
@@ -207,13 +217,13 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
             } else {
                 own_live = false;
             }
-            // Own queue empty: claim from the queue with the most tasks left;
-            // leave once every queue is empty.
+            // Own queue empty: claim from the XCD queue with the most tasks
+            // left, else from the pool; leave once all are empty.
             for (int attempt = 0; attempt < kPfClaimAttempts && task < 0; ++attempt) {
                 int rem = 0;
-                if (lane < kPfQueues) {
+                if (lane <= kPfPool) {
                     const int nhq = a.num_kv_heads > lane ? (a.num_kv_heads - lane + kPfQueues - 1) / kPfQueues : 0;
-                    const uint32_t nq = static_cast<uint32_t>(nhq * a.blocks_per_head);
+                    const uint32_t nq = static_cast<uint32_t>(lane == kPfPool ? n_pool : nhq * a.pool_block0);
                     const uint32_t c = __hip_atomic_load(a.sched + lane * kPfSchedStride, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
                     rem = static_cast<int>(nq - min(c, nq));
@@ -227,15 +237,22 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
                         best = q;
                     }
                 }
+                if (best < 0 && __shfl(rem, kPfPool) > 0) best = kPfPool;
                 if (best < 0) break;
                 uint32_t j = 0;
                 if (lane == 0)
                     j = __hip_atomic_fetch_add(a.sched + best * kPfSchedStride, 1u, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
                 j = __shfl(j, 0);
-                const int nhq = (a.num_kv_heads - best + kPfQueues - 1) / kPfQueues;
-                if (j < static_cast<uint32_t>(nhq * a.blocks_per_head))
-                    task = queue_task(best, nhq, static_cast<int>(j));
+                if (best == kPfPool) {
+                    if (j < static_cast<uint32_t>(n_pool))
+                        task = (static_cast<int>(j) % a.num_kv_heads) * a.blocks_per_head + a.pool_block0 +
+                               static_cast<int>(j) / a.num_kv_heads;
+                } else {
+                    const int nhq = (a.num_kv_heads - best + kPfQueues - 1) / kPfQueues;
+                    if (j < static_cast<uint32_t>(nhq * a.pool_block0))
+                        task = queue_task(best, nhq, static_cast<int>(j));
+                }
             }
             if (lane == 0) s_task = task;
         }
@@ -610,10 +627,10 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
         // The last workgroup to leave clears the counters for the next launch:
         // every other one has stopped claiming before its exit increment.
         if (tid == 0) {
-            const uint32_t done = __hip_atomic_fetch_add(a.sched + kPfQueues * kPfSchedStride, 1u,
+            const uint32_t done = __hip_atomic_fetch_add(a.sched + kPfExit * kPfSchedStride, 1u,
                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (done + 1 == static_cast<uint32_t>(a.n_wg)) {
-                for (int q = 0; q <= kPfQueues; ++q)
+                for (int q = 0; q < kPfSchedCounters; ++q)
                     __hip_atomic_store(a.sched + q * kPfSchedStride, 0u, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -650,6 +667,8 @@ static int32_t launch_prefill_sched(PrefillArgs a, int num_kv_heads, uint32_t* s
     a.sched = sched;
     a.n_wg = cus;
     a.num_kv_heads = num_kv_heads;
+    // The lightest quarter of each head's blocks goes to the shared pool.
+    a.pool_block0 = a.blocks_per_head - a.blocks_per_head / 4;
     hipLaunchKernelGGL((attn_prefill_kernel<false, true>), dim3(static_cast<unsigned>(cus)),
                        dim3(kPfWaves * kWave), 0, stream, a);
     return launch_status();
@@ -782,7 +801,7 @@ extern "C" int32_t grout_attn_prefill_sched(const uint16_t* q, const uint16_t* k
 }
 
 extern "C" int64_t grout_attn_prefill_sched_counter_bytes(void) {
-    return static_cast<int64_t>(kPfQueues + 1) * kPfSchedStride * 4;
+    return static_cast<int64_t>(kPfSchedCounters) * kPfSchedStride * 4;
 }
 
 extern "C" int32_t grout_attn_prefill_split(const uint16_t* q, const uint16_t* k_cache,

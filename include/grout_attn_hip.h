@@ -148,9 +148,11 @@ int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uin
                            grout_stream_t stream);
 
 /* Same computation, scheduled dynamically: one persistent workgroup per CU
- * claims workgroup-sized tasks from per-XCD queues (the KV heads
- * h = q (mod 8) in queue q, heaviest first), its own XCD's queue first, then
- * the fullest other queue, so XCDs that run faster take over the tail (the
+ * claims workgroup-sized tasks, first from its XCD's queue (the heavier three
+ * quarters of the blocks of the KV heads h = q (mod 8) for queue q, heaviest
+ * first), then from the fullest other XCD queue, then from a shared pool of
+ * every head's lighter blocks, heaviest first: XCDs that run faster take over
+ * the slower ones' heavy blocks and the last tasks are light ones (the
  * reference's LPT order, fmha_prefill_gqa_lpt src/kernels.rs:1513-1862, made
  * dynamic).  Output bit-identical to grout_attn_prefill.  Grids of at most two
  * rounds of workgroups use the static launch and leave the counters alone.
