@@ -57,6 +57,8 @@ constexpr int kPfKBytes = 16 * kPfKBlock;
 constexpr int kPfVBytes = 16 * kPfVBlock;
 constexpr int kPfStageBytes = kPfKBytes + kPfVBytes;
 constexpr int kPfStages = 4;
+constexpr int kPfOutBytes = 32 * 256;  // one wavefront's f16 output tile
+static_assert(4 * kPfOutBytes <= kPfStageBytes, "a stage holds the output tiles of 4 wavefronts");
 constexpr float kPfNegBig = -1.0e30f;
 // Lazy rescale: the running max used for p = 2^(c*s - m) is only raised when
 // some p of a tile would reach this bound (f16 holds up to 65504), so O is
@@ -127,6 +129,20 @@ __device__ __forceinline__ void lds_dma16(const void* gbase, uint32_t voff, uint
         :
         : "v"(voff), "s"(gbase), "s"(lds_base)
         : "memory");
+}
+
+// f16(f32(o / l)) for f32 o and l > 0, with rl = 1/l rounded to f64: the f64
+// product o*rl is within 2^-52 (relative) of o/l, while a quotient of two f32
+// values in the f32 normal range is never an f32 rounding midpoint and lies
+// more than 2^-49 (relative) from every one; so the product rounds to the same
+// f32 as the correctly rounded division.  Quotients below 2^-126 give +-0 in
+// f16 either way.  About 4 instructions against the ~10 of an f32 division.
+__device__ __forceinline__ half_t div_to_half(float o, double rl) {
+    float f = static_cast<float>(static_cast<double>(o) * rl);
+    // Keeps the two roundings: the code generator otherwise folds
+    // f64 -> f32 -> f16 into a single f64 -> f16 rounding, another function.
+    asm("" : "+v"(f));
+    return static_cast<half_t>(f);
 }
 
 // s_waitcnt immediate for "at most n vector-memory ops outstanding" (gfx9
@@ -315,8 +331,13 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     // clamped to the last valid row (they are masked in the softmax).
     const uint32_t lds0 = static_cast<uint32_t>(
         (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(pf_lds)));
-    const uint32_t lane_off = 4096u * static_cast<uint32_t>(lane >> 4) + 16u * (lane & 15);
-    auto issue_tile = [&](int tile, int st) {
+    // kFresh: the lane terms are derived again from the lane id at this call,
+    // so the compiler cannot hoist them out of the persistent task loop and
+    // keep (or spill) them across it; used for the prologue's two tiles.
+    auto issue_tile = [&](int tile, int st, auto fresh) {
+        int ln = lane;
+        if constexpr (decltype(fresh)::value) asm volatile("" : "+v"(ln));
+        const uint32_t lane_off = 4096u * static_cast<uint32_t>(ln >> 4) + 16u * (ln & 15);
         const uint32_t kb = lds0 + st * kPfStageBytes;
         const uint32_t vb = kb + kPfKBytes;
         const int n0 = (tile0 + tile) * kPfBN;
@@ -329,9 +350,9 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
             if (clamp) {
                 // Address from the tile start: n0 <= blk_kv_end - 1, so every
                 // clamped row is >= n0 and the unsigned offset stays in range.
-                const int row = min(n0 + blk + 16 * (lane >> 4), blk_kv_end - 1);
+                const int row = min(n0 + blk + 16 * (ln >> 4), blk_kv_end - 1);
                 row_base = static_cast<int64_t>(n0) * kHeadDim;
-                off = static_cast<uint32_t>(row - n0) * 256u + 16u * (lane & 15);
+                off = static_cast<uint32_t>(row - n0) * 256u + 16u * (ln & 15);
             }
             lds_dma16(kh + row_base, off, kb + kPfKBlock * blk);
             lds_dma16(vh + row_base, off, vb + kPfVBlock * blk);
@@ -342,8 +363,8 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     // (after the barrier that opens it), into the stage of tile t-2, whose
     // last reader (group B's PV of tile t-2, in its GEMM(t-1)) ended before
     // that barrier.
-    if (ntiles > 0) issue_tile(0, 0);
-    if (ntiles > 1) issue_tile(1, 1);
+    if (ntiles > 0) issue_tile(0, 0, std::integral_constant<bool, kDyn>{});
+    if (ntiles > 1) issue_tile(1, 1, std::integral_constant<bool, kDyn>{});
 
     // Q^T (B operand): qop[kk] = Q[row0 + l32][16kk + 8hl + 0..7].
     half8_t qop[8];
@@ -547,13 +568,13 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
         for (int t = 0; t <= ntiles; ++t) {
             open_tile_step(t);
             gemm_phase(t);
-            if (t + 2 < ntiles) issue_tile(t + 2, (t + 2) % kPfStages);
+            if (t + 2 < ntiles) issue_tile(t + 2, (t + 2) % kPfStages, std::false_type{});
             softmax_phase(t);
         }
     } else {
         for (int t = 0; t <= ntiles; ++t) {
             open_tile_step(t);
-            if (t + 2 < ntiles) issue_tile(t + 2, (t + 2) % kPfStages);
+            if (t + 2 < ntiles) issue_tile(t + 2, (t + 2) % kPfStages, std::false_type{});
             softmax_phase(t - 1);
             gemm_phase(t);
         }
@@ -565,18 +586,20 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
                                            __HIP_MEMORY_SCOPE_AGENT);
     }
     if (task_ok) {
-    // out[row][d] with d = 32db + 8(r/4) + 4hl + r%4.
-    const int row = row0 + l32;
+    // Row row0 + l32 of O^T holds dims d = 32db + 8(r/4) + 4hl + r%4.
     const float lt = l_run + swap_halves(l_run);
     const float l_safe = fmaxf(lt, 1.0e-8f);
-    // O / l_safe is a true division per element, the reference's true_div
-    // (src/kernels.rs:1289-1291).  One reciprocal and 64 multiplies measured
-    // 0.7% faster, with results up to 1 f16 ulp away: not the same operation.
+    // O / l_safe is the reference's true division (src/kernels.rs:1289-1291),
+    // rounded to f32 and then to f16: div_to_half gives that same f16 from one
+    // f64 reciprocal per row.  (An f32 reciprocal and multiplies is not the
+    // same operation: up to 1 f16 ulp away.)
+    const double rl = 1.0 / static_cast<double>(l_safe);
     if constexpr (kSplit) {
         // Logical tile (q block, head group) = bq * (Hq/GROUP) + qh/GROUP; its
         // row r = (row % BM) * GROUP + qh % GROUP in split-major scratch
         // (src/kernels.rs:2105-2141).  Rows past q_len (zero Q) are written
         // too, as the reference's padded tile rows are.
+        const int row = row0 + l32;
         const int m_eff = a.block_m * a.split_group;
         const int64_t tile = static_cast<int64_t>(row / a.block_m) * (a.num_q_heads / a.split_group) +
                              qh / a.split_group;
@@ -589,7 +612,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
             for (int i = 0; i < 4; ++i) {
                 half4_t h;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) h[e] = static_cast<half_t>(o[db][4 * i + e] / l_safe);
+                for (int e = 0; e < 4; ++e) h[e] = div_to_half(o[db][4 * i + e], rl);
                 *reinterpret_cast<half4_t*>(prow_p + 32 * db + 8 * i + 4 * hl) = h;
             }
         if (hl == 0) a.lse_partial[prow] = m_run + log2f(l_safe);
@@ -600,7 +623,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) hv[4 * db + i][e] = static_cast<half_t>(o[db][4 * i + e] / l_safe);
+                for (int e = 0; e < 4; ++e) hv[4 * db + i][e] = div_to_half(o[db][4 * i + e], rl);
         if constexpr (kDyn) {
             // The ticket claimed after the loop is read back before the
             // stores go out: vmcnt also counts stores, so reading it after
@@ -608,13 +631,40 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
             if (wave == 0) pre_ticket = own_live ? static_cast<int>(__shfl(pre_j, 0)) : -1;
             asm volatile("" ::: "memory");
         }
-        if (row < a.q_len) {
-            uint16_t* orow = a.out + (static_cast<int64_t>(row) * a.num_q_heads + qh) * kHeadDim;
+        // The 32 x 128 tile goes out in whole rows: written to LDS in the
+        // accumulator layout, read back 16 bytes a lane, so one store covers 4
+        // rows x 256 bytes.  (Stored from the accumulator layout, every store
+        // touches 32 rows, 16 bytes each: 8x the write requests, ~2 us a task.)
+        // Group A uses stage (ntiles+1) % 4, group B stage (ntiles+2) % 4: no
+        // tile is copied into either after tile ntiles-1 and their last
+        // readers ended before the last barrier.  16-byte chunk c of row r
+        // sits at chunk c ^ (r % 16), so the row reads are free of bank
+        // conflicts.
+        // Lane terms derived here from the lane id (the empty asm stops the
+        // compiler from hoisting them out of the persistent task loop and
+        // spilling them across it).
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int lr = ln & 31, lb = ln >> 4, cc = ln & 15;
+        const int sw_w = 16 * (lr & 15);
+        const int sw_r = 16 * (cc ^ lb);  // read row r = lb + 4k: r % 16 = lb | 4(k % 4)
+        unsigned char* ot = pf_lds + ((ntiles + 1 + grp) % kPfStages) * kPfStageBytes + (wave & 3) * kPfOutBytes;
+        unsigned char* wrow = ot + lr * 256 + 8 * (ln >> 5);
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    *reinterpret_cast<half4_t*>(orow + 32 * db + 8 * i + 4 * hl) = hv[4 * db + i];
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<half4_t*>(wrow + ((16 * (4 * db + i)) ^ sw_w)) = hv[4 * db + i];
+        // A wavefront's LDS accesses complete in order; the fence keeps the
+        // compiler from moving the reads above the writes.
+        asm volatile("" ::: "memory");
+        const unsigned char* rrow = ot + lb * 256;
+        uint16_t* orow = a.out + (static_cast<int64_t>(row0 + lb) * a.num_q_heads + qh) * kHeadDim + 8 * cc;
+        const int64_t ostep = static_cast<int64_t>(4) * a.num_q_heads * kHeadDim;  // 4 rows
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint4_t v = *reinterpret_cast<const uint4_t*>(rrow + 1024 * k + (sw_r ^ (64 * (k & 3))));
+            if (row0 + lb + 4 * k < a.q_len) *reinterpret_cast<uint4_t*>(orow + ostep * k) = v;
         }
     }
     } else if constexpr (kDyn) {
