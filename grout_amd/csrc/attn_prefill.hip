@@ -100,17 +100,20 @@ struct PrefillArgs {
 };
 
 // Dynamic schedule.  A task is a workgroup-sized unit (one block of the static
-// grid).  Blocks [0, pool_block0) of the KV heads h = q (mod kPfQueues) form
-// XCD queue q, heaviest first; the lighter blocks [pool_block0, blocks_per_head)
-// of every head form one shared pool, heaviest first with the heads
-// interleaved.  A persistent workgroup claims from the queue of the XCD it
-// runs on (a head's K/V stay in that XCD's L2), then from the fullest other
-// XCD queue, then from the pool: XCDs that run faster take over the slower
-// ones' heavy blocks, and the last tasks anywhere are the lightest ones.
+// grid).  The KV heads h = q (mod kPfQueues) belong to XCD q: their blocks
+// [0, pool_block0) form its heavy queue and the lighter blocks
+// [pool_block0, blocks_per_head) its light queue, each heaviest first with the
+// heads interleaved.  A persistent workgroup claims from the heavy queue of
+// the XCD it runs on (a head's K/V stay in that XCD's L2), then from the
+// fullest other heavy queue, then from its own light queue while that holds
+// at least half as many tasks as the fullest light queue, else from the
+// fullest: XCDs that run faster take over the slower ones' heavy blocks, the
+// last tasks anywhere are light ones, and most light tasks still run where
+// their head's K/V are cached.
 constexpr int kPfQueues = 8;
-constexpr int kPfPool = kPfQueues;          // counter index of the shared pool
-constexpr int kPfExit = kPfQueues + 1;      // counter index of the exit counter
-constexpr int kPfSchedCounters = kPfQueues + 2;
+constexpr int kPfLight = kPfQueues;             // counter index of light queue q: kPfLight + q
+constexpr int kPfExit = 2 * kPfQueues;          // counter index of the exit counter
+constexpr int kPfSchedCounters = 2 * kPfQueues + 1;
 constexpr int kPfSchedStride = 64;  // u32: one 256-byte line per counter
 constexpr int kPfClaimAttempts = 64;
 
@@ -216,12 +219,12 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
                                            __HIP_MEMORY_SCOPE_AGENT);
         if (wave == 0 && own_live) pre_ticket = static_cast<int>(__shfl(pre_j, 0));
     }
-    // Task j of XCD queue q: KV head q + kPfQueues*(j % nhq), block j / nhq;
-    // task j of the pool: KV head j % Hkv, block pool_block0 + j / Hkv.
+    // Task j of heavy queue q: KV head q + kPfQueues*(j % nhq), block j / nhq;
+    // of light queue q: the same head, block pool_block0 + j / nhq.
     auto queue_task = [&](int q, int nhq, int j) {
         return (q + kPfQueues * (j % nhq)) * a.blocks_per_head + j / nhq;
     };
-    const int n_pool = a.num_kv_heads * (a.blocks_per_head - a.pool_block0);
+    const int light_blocks = a.blocks_per_head - a.pool_block0;
 
     for (;;) {
     if constexpr (kDyn) {
@@ -229,17 +232,24 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
             int task = -1;
             const int j0 = pre_ticket;
             if (own_live && j0 >= 0 && j0 < nq_own) {
-                task = queue_task(my_q, nhq_own, j0);
+                // nhq_own passes through an empty asm so that the division's
+                // constants are derived here, not held across the task loop.
+                int nhq = nhq_own;
+                asm volatile("" : "+s"(nhq));
+                task = queue_task(my_q, nhq, j0);
             } else {
                 own_live = false;
             }
-            // Own queue empty: claim from the XCD queue with the most tasks
-            // left, else from the pool; leave once all are empty.
+            // Own heavy queue empty: claim from the fullest other heavy queue,
+            // else from the own light queue if it holds at least half as many
+            // tasks as the fullest light queue, else from the fullest; leave
+            // once all are empty.  Lane i < 2*kPfQueues reads counter i.
             for (int attempt = 0; attempt < kPfClaimAttempts && task < 0; ++attempt) {
                 int rem = 0;
-                if (lane <= kPfPool) {
-                    const int nhq = a.num_kv_heads > lane ? (a.num_kv_heads - lane + kPfQueues - 1) / kPfQueues : 0;
-                    const uint32_t nq = static_cast<uint32_t>(lane == kPfPool ? n_pool : nhq * a.pool_block0);
+                if (lane < 2 * kPfQueues) {
+                    const int q = lane % kPfQueues;
+                    const int nhq = a.num_kv_heads > q ? (a.num_kv_heads - q + kPfQueues - 1) / kPfQueues : 0;
+                    const uint32_t nq = static_cast<uint32_t>(nhq * (lane < kPfQueues ? a.pool_block0 : light_blocks));
                     const uint32_t c = __hip_atomic_load(a.sched + lane * kPfSchedStride, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
                     rem = static_cast<int>(nq - min(c, nq));
@@ -253,21 +263,30 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
                         best = q;
                     }
                 }
-                if (best < 0 && __shfl(rem, kPfPool) > 0) best = kPfPool;
+                if (best < 0) {
+#pragma unroll
+                    for (int q = 0; q < kPfQueues; ++q) {
+                        const int r = __shfl(rem, kPfLight + q);
+                        if (r > best_rem) {
+                            best_rem = r;
+                            best = kPfLight + q;
+                        }
+                    }
+                    const int own_rem = __shfl(rem, kPfLight + my_q);
+                    if (own_rem > 0 && (own_rem << 1) >= best_rem) best = kPfLight + my_q;
+                }
                 if (best < 0) break;
                 uint32_t j = 0;
                 if (lane == 0)
                     j = __hip_atomic_fetch_add(a.sched + best * kPfSchedStride, 1u, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
                 j = __shfl(j, 0);
-                if (best == kPfPool) {
-                    if (j < static_cast<uint32_t>(n_pool))
-                        task = (static_cast<int>(j) % a.num_kv_heads) * a.blocks_per_head + a.pool_block0 +
-                               static_cast<int>(j) / a.num_kv_heads;
-                } else {
-                    const int nhq = (a.num_kv_heads - best + kPfQueues - 1) / kPfQueues;
-                    if (j < static_cast<uint32_t>(nhq * a.pool_block0))
-                        task = queue_task(best, nhq, static_cast<int>(j));
+                const int q = best % kPfQueues;
+                const int nhq = (a.num_kv_heads - q + kPfQueues - 1) / kPfQueues;
+                if (best < kPfQueues) {
+                    if (j < static_cast<uint32_t>(nhq * a.pool_block0)) task = queue_task(q, nhq, static_cast<int>(j));
+                } else if (j < static_cast<uint32_t>(nhq * light_blocks)) {
+                    task = queue_task(q, nhq, static_cast<int>(j)) + a.pool_block0;
                 }
             }
             if (lane == 0) s_task = task;

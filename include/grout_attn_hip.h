@@ -148,14 +148,17 @@ int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uin
                            grout_stream_t stream);
 
 /* Same computation, scheduled dynamically: one persistent workgroup per CU
- * claims workgroup-sized tasks, first from its XCD's queue (the heavier three
- * quarters of the blocks of the KV heads h = q (mod 8) for queue q, heaviest
- * first), then from the fullest other XCD queue, then from a shared pool of
- * every head's lighter blocks, heaviest first: XCDs that run faster take over
- * the slower ones' heavy blocks and the last tasks are light ones (the
- * reference's LPT order, fmha_prefill_gqa_lpt src/kernels.rs:1513-1862, made
- * dynamic).  Output bit-identical to grout_attn_prefill.  Grids of at most two
- * rounds of workgroups use the static launch and leave the counters alone.
+ * claims workgroup-sized tasks.  XCD q owns the KV heads h = q (mod 8): the
+ * heavier three quarters of their blocks form its heavy queue, the lighter
+ * quarter its light queue, each heaviest first.  A workgroup claims from its
+ * XCD's heavy queue, then from the fullest other heavy queue, then from its
+ * own light queue while that holds at least half as many tasks as the fullest
+ * light queue, else from the fullest: XCDs that run faster take over the
+ * slower ones' heavy blocks, the last tasks are light ones, and most tasks run
+ * where their head's K/V are cached (the reference's LPT order,
+ * fmha_prefill_gqa_lpt src/kernels.rs:1513-1862, made dynamic).  Output
+ * bit-identical to grout_attn_prefill.  Grids of at most two rounds of
+ * workgroups use the static launch and leave the counters alone.
  *   sched_counters: grout_attn_prefill_sched_counter_bytes() bytes, 4-byte
  *   aligned, zero before the first call; every call leaves them zero.
  * Calls that overlap on one set of counters race. */

@@ -130,8 +130,8 @@ def test_prefill_sched_checks(L):
     assert call(kv=17) == -6
     assert call(sc=0.0) == -9
     assert call(ql=0) == 0
-    # 8 XCD queues, the shared pool and the exit counter, one 256-byte line each.
-    assert L.grout_attn_prefill_sched_counter_bytes() == 10 * 256
+    # 8 heavy and 8 light XCD queues and the exit counter, one 256-byte line each.
+    assert L.grout_attn_prefill_sched_counter_bytes() == 17 * 256
 
 
 def test_prefill_split_checks(L):

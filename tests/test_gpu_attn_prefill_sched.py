@@ -7,7 +7,8 @@ oracle (src/kernels.rs:1146-1295); one case also checks sampled rows against
 the oracle directly.  The counters must be zero again after every call, and
 grids of at most two rounds of workgroups must take the static launch without
 touching them.  Shapes cover one KV head per queue (Hkv 8), empty queues that
-are drained by stealing from the start (Hkv 4), two heads per queue (Hkv 16),
+are drained by stealing from the start (Hkv 4, and Hkv 1 where seven XCDs own
+nothing), two heads per queue (Hkv 16), three heads with a ragged last block,
 a chunk at query_start > 0, and two calls in a row on one buffer (all of
 them grids of more than two rounds of workgroups on 256 CUs).
 """
@@ -38,7 +39,9 @@ def _inputs(torch, seed, q_len, hq, hkv, ms, outliers=False):
     (6144, 32, 4, 0, True),      # queues 4-7 empty: their workgroups steal from the start
     (4096, 64, 16, 0, False),    # two KV heads per queue, interleaved
     (6144, 32, 8, 1000, False),  # a chunk at query_start > 0
-], ids=["c3", "hkv4", "hkv16", "chunk"])
+    (20000, 8, 1, 0, False),     # one KV head: seven XCDs steal every heavy and light task
+    (12000, 12, 3, 0, True),     # three KV heads, G = 4, ragged last block
+], ids=["c3", "hkv4", "hkv16", "chunk", "hkv1", "hkv3"])
 def test_sched_bit_identical_to_static(gpu, q_len, hq, hkv, qs, outliers):
     import torch
 
