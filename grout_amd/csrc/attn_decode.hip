@@ -277,12 +277,27 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     const uint32_t pos = pos_raw < static_cast<uint32_t>(a.max_seq_len) ? pos_raw
                                                                          : a.max_seq_len - 1;
     const int s_kv = static_cast<int>(pos) + 1;
-    const int tiles = (s_kv + a.block_n - 1) / a.block_n;
-    const int per = (tiles + a.num_splits - 1) / a.num_splits;
-    const int tb = split * per;
-    const int te = min(tb + per, tiles);
-    const int tok_begin = tb * a.block_n;
-    const int tok_end = (tb < te) ? min(te * a.block_n, s_kv) : tok_begin;
+    int tok_begin, tok_end;
+    if constexpr (kFused) {
+        // The fused form's partials never leave the launch, so its splits
+        // are balanced in 16-token sub-chunks: split s takes sub-chunks
+        // [s*n/NKS, (s+1)*n/NKS) of n = ceil(s_kv/16).  The reference's
+        // ceil(tiles/NKS) tiles per split leaves the last splits short or
+        // empty (s_kv 4097, BN 32, 32 splits: 25 splits of 160 tokens, one of
+        // 97 and six empty; here 128-129 tokens each).
+        const int64_t nsub_all = (s_kv + kDecSubTok - 1) / kDecSubTok;
+        const int sb = static_cast<int>(split * nsub_all / a.num_splits);
+        const int se = static_cast<int>((split + 1) * nsub_all / a.num_splits);
+        tok_begin = sb * kDecSubTok;
+        tok_end = (sb < se) ? min(se * kDecSubTok, s_kv) : tok_begin;
+    } else {
+        const int tiles = (s_kv + a.block_n - 1) / a.block_n;
+        const int per = (tiles + a.num_splits - 1) / a.num_splits;
+        const int tb = split * per;
+        const int te = min(tb + per, tiles);
+        tok_begin = tb * a.block_n;
+        tok_end = (tb < te) ? min(te * a.block_n, s_kv) : tok_begin;
+    }
     const int nsub = (tok_end - tok_begin + kDecSubTok - 1) / kDecSubTok;
     // The first kDecWaveStages sub-chunks of each wavefront are fixed
     // (w, w+4, w+8, w+12); after that a wavefront takes the next untaken

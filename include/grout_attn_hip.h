@@ -289,8 +289,11 @@ int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_pa
  * (src/model.rs:3194-3221, 3428-3473): RMSNorm + RoPE of the G query rows of
  * each KV head (q_out rows [0, num_q_heads) are written, as A3 does), the
  * K/V-cache write at *d_position, split-K GQA attention over s_kv =
- * *d_position + 1 keys into att_partial/lse_partial (same layout and split
- * boundaries as grout_attn_decode_split) and the LSE merge into out
+ * *d_position + 1 keys into att_partial/lse_partial (same layout as
+ * grout_attn_decode_split; the partials are scratch of this launch, so its
+ * splits are balanced instead: split s covers the 16-token sub-chunks
+ * [s*n/num_splits, (s+1)*n/num_splits) of n = ceil(s_kv/16), and block_n is
+ * only validated) and the LSE merge into out
  * [num_kv_heads, group, 128].  The last workgroup of each KV head merges: it
  * is found by an agent-scope counter in `counters`, and the partials reach it
  * through device-coherent stores completed before that counter moves.

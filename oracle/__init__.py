@@ -54,7 +54,8 @@ def lib():
         L.go_attn_prefill_f32.argtypes = (
             [_u16p] * 3 + [_f32p, ctypes.c_float] + [_i32] * 10)
         L.go_attn_decode_split.argtypes = (
-            [_u16p] * 4 + [_f32p, ctypes.c_uint16, ctypes.c_uint32] + [_i32] * 7)
+            [_u16p] * 4 + [_f32p, ctypes.c_uint16, ctypes.c_uint32] + [_i32] * 8)
+        L.go_decode_split_range_fused.argtypes = [_i32] * 3 + [ctypes.POINTER(_i32)] * 2
         L.go_attn_decode_merge.argtypes = [_u16p, _f32p, _u16p] + [_i32] * 4
         L.go_decode_split_range.argtypes = [_i32] * 4 + [ctypes.POINTER(_i32)] * 2
         L.go_kv_cache_update_seq.argtypes = [_u16p] * 4 + [_i32] * 5
@@ -149,15 +150,18 @@ def attn_prefill_f32(q, k_cache, v_cache, qk_scale: float, kv_len: int, query_st
 
 
 def attn_decode_split(q, k_cache, v_cache, qk_scale_f16_bits: int, position: int,
-                      block_n: int, num_splits: int, nthreads: int = 0):
-    """q [Hkv, G, D] f16 -> (att_partial [Hkv, NKS*G, D] f16, lse [Hkv, NKS*G] f32)."""
+                      block_n: int, num_splits: int, nthreads: int = 0,
+                      fused_ranges: bool = False):
+    """q [Hkv, G, D] f16 -> (att_partial [Hkv, NKS*G, D] f16, lse [Hkv, NKS*G] f32).
+    fused_ranges: the split boundaries of the fused decode step
+    (decode_split_range_fused) instead of the reference's."""
     Hkv, G, D = q.shape
     max_seq = k_cache.shape[1]
     att = np.zeros((Hkv, num_splits * G, D), dtype=np.float16)
     lse = np.zeros((Hkv, num_splits * G), dtype=np.float32)
     lib().go_attn_decode_split(
         _u16(q), _u16(k_cache), _u16(v_cache), _u16(att), _f32(lse), qk_scale_f16_bits,
-        position, Hkv, G, D, max_seq, block_n, num_splits, nthreads)
+        position, Hkv, G, D, max_seq, block_n, num_splits, nthreads, int(bool(fused_ranges)))
     return att, lse
 
 
@@ -167,6 +171,14 @@ def attn_decode_merge(att, lse, group: int) -> np.ndarray:
     out = np.zeros((Hkv, group, D), dtype=np.float16)
     lib().go_attn_decode_merge(_u16(att), _f32(lse), _u16(out), Hkv, group, D, ns)
     return out
+
+
+def decode_split_range_fused(s_kv: int, num_splits: int, split: int):
+    """Token range [b, e) of a split in the fused decode step (balanced 16-token
+    sub-chunks; this repository's choice, not the reference's)."""
+    b, e = _i32(), _i32()
+    lib().go_decode_split_range_fused(s_kv, num_splits, split, ctypes.byref(b), ctypes.byref(e))
+    return b.value, e.value
 
 
 def decode_split_range(s_kv: int, block_n: int, num_splits: int, split: int):
@@ -235,13 +247,15 @@ def silu_mul(gate, up) -> np.ndarray:
     return out
 
 
-def qwen3_decode_step(model: dict, token: int, position: int, block_n: int, num_splits: int):
+def qwen3_decode_step(model: dict, token: int, position: int, block_n: int, num_splits: int,
+                      fused_ranges: bool = False):
     """One decode token step of src/model.rs:3118-3648, composed of this
     oracle's ops in the graph's order.  `model` holds numpy f16 arrays
     (embed_tokens, final_norm, lm_head, inv_freq (f32), layers: list of dicts
     with input_norm, qkv_proj, q_norm, k_norm, o_proj, post_attn_norm,
     gate_up_proj, down_proj, k_cache, v_cache) and eps, qk_scale_f16_bits,
     num_q_heads, num_kv_heads.  Writes the caches at `position` in place.
+    fused_ranges: attention splits on the fused decode step's boundaries.
     Returns (logits f16 [vocab], next token)."""
     hq, hkv, eps = model["num_q_heads"], model["num_kv_heads"], model["eps"]
     D = 128
@@ -259,7 +273,7 @@ def qwen3_decode_step(model: dict, token: int, position: int, block_n: int, num_
                                L["k_cache"], L["v_cache"], position, eps, hq, hkv)
         qg = q_out[:hq * D].reshape(hkv, G, D)
         att, lse = attn_decode_split(qg, L["k_cache"], L["v_cache"], model["qk_scale_f16_bits"],
-                                     position, block_n, num_splits)
+                                     position, block_n, num_splits, fused_ranges=fused_ranges)
         attn_out = attn_decode_merge(att, lse, G).reshape(-1)
         attn_proj = gemv_f16(L["o_proj"], attn_out)          # :3505-3511
         normed, hidden_after_attn = add_rms_norm(hidden, attn_proj, L["post_attn_norm"], eps)

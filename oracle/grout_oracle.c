@@ -282,6 +282,15 @@ void go_decode_split_range(int32_t s_kv, int32_t block_n, int32_t num_splits, in
     *tile_end = e;
 }
 
+void go_decode_split_range_fused(int32_t s_kv, int32_t num_splits, int32_t split,
+                                 int32_t* tok_begin, int32_t* tok_end) {
+    int64_t n = ((int64_t)s_kv + 15) / 16;
+    int32_t b = (int32_t)(split * n / num_splits);
+    int32_t e = (int32_t)((split + 1) * n / num_splits);
+    *tok_begin = 16 * b;
+    *tok_end = b < e ? (16 * e < s_kv ? 16 * e : s_kv) : 16 * b;
+}
+
 /* src/kernels.rs:2586-2749 fmha_decode_gqa_split, one (kv_head, split) per task.
  *   scale_log2 = f32(qk_scale_f16) / ln(2)                       (:2618-2622)
  *   m = -1e30, l[BN][G] = 1, acc[G][D] = 0                        (:2635-2639)
@@ -291,15 +300,16 @@ void go_decode_split_range(int32_t s_kv, int32_t block_n, int32_t num_splits, in
  *   acc = acc*alpha + sum_n f16(p)*v                               (:2687-2722)
  *   O = f16(acc / max(sum_n l, 1e-8)); LSE = m + log2(max(sum_n l, 1e-8)) (:2729-2748)
  * Cache slots at or beyond max_seq_len read as 0 (tile loads past the view are
- * zero-filled). */
+ * zero-filled).  The split's tokens [b, e) run in BN-token tiles from b, and
+ * slots at or past e get the -1e30; with the reference's boundaries that is
+ * exactly its rule (only the last global tile has slots past s_kv). */
 void go_attn_decode_split(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                           uint16_t* att_partial, float* lse_partial, uint16_t qk_scale_f16,
                           uint32_t position, int32_t num_kv_heads, int32_t group,
                           int32_t head_dim, int32_t max_seq_len, int32_t block_n,
-                          int32_t num_splits, int32_t nthreads) {
+                          int32_t num_splits, int32_t nthreads, int32_t fused_ranges) {
     const int32_t D = head_dim, G = group, BN = block_n;
     const int32_t s_kv = (int32_t)position + 1;
-    const int32_t tiles = (s_kv + BN - 1) / BN;
     const float ln2 = logf(2.0f);
     const float scale_log2 = h2f(qk_scale_f16) / ln2;
     int64_t tasks = (int64_t)num_kv_heads * num_splits;
@@ -321,8 +331,15 @@ void go_attn_decode_split(const uint16_t* q, const uint16_t* k_cache, const uint
         for (int64_t t = 0; t < tasks; ++t) {
             int32_t kvh = (int32_t)(t / num_splits);
             int32_t split = (int32_t)(t % num_splits);
-            int32_t tb, te;
-            go_decode_split_range(s_kv, BN, num_splits, split, &tb, &te);
+            int32_t b, e;
+            if (fused_ranges) {
+                go_decode_split_range_fused(s_kv, num_splits, split, &b, &e);
+            } else {
+                int32_t tb, te;
+                go_decode_split_range(s_kv, BN, num_splits, split, &tb, &te);
+                b = tb * BN;
+                e = tb < te ? (te * BN < s_kv ? te * BN : s_kv) : b;
+            }
             for (int32_t i = 0; i < G * D; ++i) {
                 qf[i] = h2f(q[(int64_t)kvh * G * D + i]);
                 acc[i] = 0.0f;
@@ -331,9 +348,9 @@ void go_attn_decode_split(const uint16_t* q, const uint16_t* k_cache, const uint
             for (int32_t i = 0; i < BN * G; ++i) l[i] = 1.0f;
             const uint16_t* kh = k_cache + (int64_t)kvh * max_seq_len * D;
             const uint16_t* vh = v_cache + (int64_t)kvh * max_seq_len * D;
-            for (int32_t j = tb; j < te; ++j) {
+            for (int32_t t0 = b; t0 < e; t0 += BN) {
                 for (int32_t n = 0; n < BN; ++n) {
-                    int32_t tok = j * BN + n;
+                    int32_t tok = t0 + n;
                     for (int32_t d = 0; d < D; ++d) {
                         kt[n * D + d] = tok < max_seq_len ? h2f(kh[(int64_t)tok * D + d]) : 0.0f;
                         vt[n * D + d] = tok < max_seq_len ? h2f(vh[(int64_t)tok * D + d]) : 0.0f;
@@ -345,9 +362,9 @@ void go_attn_decode_split(const uint16_t* q, const uint16_t* k_cache, const uint
                         for (int32_t d = 0; d < D; ++d) dot += kt[n * D + d] * qf[g * D + d];
                         qk[n * G + g] = dot;
                     }
-                if (j == tiles - 1) {
+                if (t0 + BN > e) {
                     for (int32_t n = 0; n < BN; ++n) {
-                        float add = (j * BN + n < s_kv) ? 0.0f : (0.0f - 1.0e30f);
+                        float add = (t0 + n < e) ? 0.0f : (0.0f - 1.0e30f);
                         for (int32_t g = 0; g < G; ++g) qk[n * G + g] = qk[n * G + g] + add;
                     }
                 }

@@ -61,12 +61,20 @@ void go_attn_prefill_f32(const uint16_t* q, const uint16_t* k_cache, const uint1
 /* src/kernels.rs:2586-2749 fmha_decode_gqa_split.  q [Hkv,G,D] (first Hq*D of
  * q_out); att_partial [Hkv, NKS*G, D] f16 split-major (split*G+g);
  * lse_partial [Hkv, NKS*G] f32 in log2 units.  qk_scale_f16 is the f16 bit
- * pattern of the scale (src/model.rs:3427 rounds 1/sqrt(D) to f16). */
+ * pattern of the scale (src/model.rs:3427 rounds 1/sqrt(D) to f16).
+ * fused_ranges = 0: the reference's split boundaries (go_decode_split_range);
+ * 1: the boundaries of this repository's fused decode step (no counterpart in
+ * the reference; go_decode_split_range_fused), same per-split arithmetic. */
 void go_attn_decode_split(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                           uint16_t* att_partial, float* lse_partial, uint16_t qk_scale_f16,
                           uint32_t position, int32_t num_kv_heads, int32_t group,
                           int32_t head_dim, int32_t max_seq_len, int32_t block_n,
-                          int32_t num_splits, int32_t nthreads);
+                          int32_t num_splits, int32_t nthreads, int32_t fused_ranges);
+
+/* Token range [begin, end) of split `split` in the fused decode step: n =
+ * ceil(s_kv/16) sub-chunks of 16 tokens, split s takes [s*n/NKS, (s+1)*n/NKS). */
+void go_decode_split_range_fused(int32_t s_kv, int32_t num_splits, int32_t split,
+                                 int32_t* tok_begin, int32_t* tok_end);
 
 /* src/kernels.rs:2771-2868 splitk_reduce_merge.  out [Hkv, G, D] f16. */
 void go_attn_decode_merge(const uint16_t* att_partial, const float* lse_partial, uint16_t* out,

@@ -262,15 +262,20 @@ def test_fused_step_matches_oracle(gpu, hq, hkv, pos, MS, ns, seed):
     assert np.array_equal(vc_dev.view(np.uint16), vc_ref.view(np.uint16))
     assert f16_ulp_diff(kc_dev, kc_ref).max() <= 1
     qg = np.ascontiguousarray(qo_ref[:hq].reshape(hkv, G, D))
-    a_ref, l_ref = oracle.attn_decode_split(qg, kc_ref, vc_ref, qk_scale_f16_bits(), pos, BN, ns)
-    s_kv = pos + 1
-    nonempty = np.array([oracle.decode_split_range(s_kv, BN, ns, s)[0]
-                         < oracle.decode_split_range(s_kv, BN, ns, s)[1] for s in range(ns)])
-    rows = np.repeat(nonempty, G)
+    # The fused form's partials stay inside the launch and its splits are
+    # balanced 16-token ranges: the partials are held to the oracle's split
+    # arithmetic on those ranges, the merged output to the oracle's split +
+    # merge on the reference's ranges and to an f32 attention.
+    ranges = [oracle.decode_split_range_fused(pos + 1, ns, s) for s in range(ns)]
+    a_ref, l_ref = oracle.attn_decode_split(qg, kc_ref, vc_ref, qk_scale_f16_bits(), pos, BN, ns,
+                                            fused_ranges=True)
+    rows = np.repeat(np.array([b < e for b, e in ranges]), G)
     a_dev, l_dev = att.cpu().numpy(), lse.cpu().numpy()
     assert_close_attn(a_dev[:, rows], a_ref[:, rows], "fused att_partial")
     assert np.max(np.abs(l_dev[:, rows] - l_ref[:, rows])) < 1e-3
-    out_ref = oracle.attn_decode_merge(a_ref, l_ref, G)
+    assert np.all(l_dev[:, ~rows] == np.float32(-1e30))
+    a_o, l_o = oracle.attn_decode_split(qg, kc_ref, vc_ref, qk_scale_f16_bits(), pos, BN, ns)
+    out_ref = oracle.attn_decode_merge(a_o, l_o, G)
     assert_close_attn(out.cpu().numpy(), out_ref, "fused out vs oracle")
     assert_close_attn(out.cpu().numpy(), _fp32_decode(qg, kc_ref, vc_ref, pos),
                       "fused out vs fp32 decode")

@@ -131,7 +131,7 @@ def test_token_step_from_checkpoint(gpu, tmp_path):
         for pos in range(4):
             if pos:
                 runner.step(pos)
-            rl, _ = oracle.qwen3_decode_step(ref, tok, pos, 32, 2)
+            rl, _ = oracle.qwen3_decode_step(ref, tok, pos, 32, 2, fused_ranges=True)
             gl = logits.cpu().numpy()
             assert_close_attn(gl, rl, f"position {pos} logits", atol=1e-2, rtol=1e-2)
             tok = int(token.item())

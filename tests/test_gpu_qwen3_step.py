@@ -7,7 +7,8 @@ Contract:
 * embed + norm: residual_out bit-exact (a row copy), out within 1 f16 ulp;
 * SiLU * up within 1 f16 ulp;
 * token step (a 2-layer model, random weights): logits within 1e-2 + 1e-2|x|
-  of the oracle's composed step fed the same token, the picked token equal to
+  of the oracle's composed step fed the same token (its attention split on
+  the fused decode step's balanced boundaries), the picked token equal to
   the argmax of the logits the GPU produced, the caches written at each step's
   position within 2e-2 of the oracle's (bit-exact elsewhere), and the device
   position advanced once per step.  Graph replays, eager steps and replays
@@ -102,7 +103,7 @@ def test_token_step_graph_matches_oracle(gpu):
     try:
         torch.cuda.synchronize()
         written = [p0]
-        rl, _ = oracle.qwen3_decode_step(ref, t0, p0, bn, ns)
+        rl, _ = oracle.qwen3_decode_step(ref, t0, p0, bn, ns, fused_ranges=True)
         gl = logits.cpu().numpy()
         assert_close_attn(gl, rl, "prime step logits", atol=1e-2, rtol=1e-2)
         tok = int(token.item())
@@ -111,7 +112,7 @@ def test_token_step_graph_matches_oracle(gpu):
         # launch_step: one replay per call, the token read back.
         for i in range(1, 4):
             nxt = runner.step(p0 + i)
-            rl, _ = oracle.qwen3_decode_step(ref, tok, p0 + i, bn, ns)
+            rl, _ = oracle.qwen3_decode_step(ref, tok, p0 + i, bn, ns, fused_ranges=True)
             gl = logits.cpu().numpy()
             assert_close_attn(gl, rl, f"replay {i} logits", atol=1e-2, rtol=1e-2)
             assert nxt == oracle.argmax_f16(gl) == int(token.item())
@@ -122,7 +123,7 @@ def test_token_step_graph_matches_oracle(gpu):
         # An eager step on the runner's stream matches the oracle the same way.
         runner.eager_step()
         torch.cuda.synchronize()
-        rl, _ = oracle.qwen3_decode_step(ref, tok, p0 + 4, bn, ns)
+        rl, _ = oracle.qwen3_decode_step(ref, tok, p0 + 4, bn, ns, fused_ranges=True)
         gl = logits.cpu().numpy()
         assert_close_attn(gl, rl, "eager step logits", atol=1e-2, rtol=1e-2)
         tok = int(token.item())
@@ -131,14 +132,14 @@ def test_token_step_graph_matches_oracle(gpu):
         # follows the token chain the GPU picked (read from the final state).
         runner.seed_token(5)
         runner.step(p0 + 5)
-        rl, _ = oracle.qwen3_decode_step(ref, 5, p0 + 5, bn, ns)
+        rl, _ = oracle.qwen3_decode_step(ref, 5, p0 + 5, bn, ns, fused_ranges=True)
         assert_close_attn(logits.cpu().numpy(), rl, "seeded step logits", atol=1e-2, rtol=1e-2)
         tok = int(token.item())
         runner.run(p0 + 6, 3)
         torch.cuda.synchronize()
         assert int(position.item()) == p0 + 9
         for i in range(6, 9):
-            rl, t = oracle.qwen3_decode_step(ref, tok, p0 + i, bn, ns)
+            rl, t = oracle.qwen3_decode_step(ref, tok, p0 + i, bn, ns, fused_ranges=True)
             tok = t
         gl = logits.cpu().numpy()
         assert_close_attn(gl, rl, "back-to-back replay logits", atol=1e-2, rtol=1e-2)
@@ -166,11 +167,11 @@ def test_token_step_single_layer_gqa8(gpu):
         prime_position=100)
     try:
         torch.cuda.synchronize()
-        rl, _ = oracle.qwen3_decode_step(ref, 77, 100, 32, 4)
+        rl, _ = oracle.qwen3_decode_step(ref, 77, 100, 32, 4, fused_ranges=True)
         assert_close_attn(logits.cpu().numpy(), rl, "prime logits", atol=1e-2, rtol=1e-2)
         tok = int(token.item())
         nxt = runner.step(101)
-        rl, _ = oracle.qwen3_decode_step(ref, tok, 101, 32, 4)
+        rl, _ = oracle.qwen3_decode_step(ref, tok, 101, 32, 4, fused_ranges=True)
         gl = logits.cpu().numpy()
         assert_close_attn(gl, rl, "replay logits", atol=1e-2, rtol=1e-2)
         assert nxt == oracle.argmax_f16(gl)
@@ -204,7 +205,7 @@ def test_token_step_qwen3_06b_shapes(gpu):
         for pos in (30, 31, 32):
             if pos > 30:
                 runner.step(pos)
-            rl, _ = oracle.qwen3_decode_step(ref, tok, pos, 32, 2)
+            rl, _ = oracle.qwen3_decode_step(ref, tok, pos, 32, 2, fused_ranges=True)
             gl = logits.cpu().numpy()
             assert_close_attn(gl, rl, f"position {pos} logits", atol=1e-2, rtol=1e-2)
             tok = int(token.item())
@@ -235,20 +236,20 @@ def test_runner_step_after_eager_step_writes_position(gpu):
     try:
         torch.cuda.synchronize()
         # The oracle follows the token chain the GPU picked.
-        oracle.qwen3_decode_step(ref, 9, 40, 32, 3)
+        oracle.qwen3_decode_step(ref, 9, 40, 32, 3, fused_ranges=True)
         t_in = int(token.item())
         runner.step(41)
-        oracle.qwen3_decode_step(ref, t_in, 41, 32, 3)
+        oracle.qwen3_decode_step(ref, t_in, 41, 32, 3, fused_ranges=True)
         # Eager step at 41 + 1 = 42; the device position ends at 43.
         t_in = int(token.item())
         runner.eager_step()
         runner.stream.synchronize()
         assert int(position.item()) == 43
-        oracle.qwen3_decode_step(ref, t_in, 42, 32, 3)
+        oracle.qwen3_decode_step(ref, t_in, 42, 32, 3, fused_ranges=True)
         # A step at 42 again: the runner must write the position.
         t_in = int(token.item())
         nxt = runner.step(42)
-        rl, _ = oracle.qwen3_decode_step(ref, t_in, 42, 32, 3)
+        rl, _ = oracle.qwen3_decode_step(ref, t_in, 42, 32, 3, fused_ranges=True)
         gl = logits.cpu().numpy()
         assert_close_attn(gl, rl, "step after eager step", atol=1e-2, rtol=1e-2)
         assert nxt == oracle.argmax_f16(gl)
@@ -280,13 +281,13 @@ def test_runner_picked_splits_two_kv_heads_multi_batch_merge(gpu):
         prime_position=4100)
     try:
         torch.cuda.synchronize()
-        rl, _ = oracle.qwen3_decode_step(ref, 3, 4100, 32, ns)
+        rl, _ = oracle.qwen3_decode_step(ref, 3, 4100, 32, ns, fused_ranges=True)
         gl = logits.cpu().numpy()
         assert_close_attn(gl, rl, "prime logits", atol=1e-2, rtol=1e-2)
         tok = int(token.item())
         assert tok == oracle.argmax_f16(gl)
         nxt = runner.step(4101)
-        rl, _ = oracle.qwen3_decode_step(ref, tok, 4101, 32, ns)
+        rl, _ = oracle.qwen3_decode_step(ref, tok, 4101, 32, ns, fused_ranges=True)
         gl = logits.cpu().numpy()
         assert_close_attn(gl, rl, "replay logits", atol=1e-2, rtol=1e-2)
         assert nxt == oracle.argmax_f16(gl)

@@ -276,6 +276,49 @@ def test_split_merge_matches_float64_decode(ns):
             assert np.max(np.abs(lse[h, rows] - lse_ref)) < 1e-4
 
 
+def test_fused_split_ranges_partition_tokens():
+    """The fused decode step's boundaries (not the reference's): contiguous
+    16-token-aligned ranges covering [0, s_kv), sizes within one sub-chunk."""
+    for s_kv in (1, 15, 16, 17, 4097, 32769):
+        for ns in (1, 3, 16, 32, 200):
+            ranges = [oracle.decode_split_range_fused(s_kv, ns, s) for s in range(ns)]
+            covered = []
+            for b, e in ranges:
+                assert b % 16 == 0 and b <= e
+                covered.extend(range(b, e))
+            assert covered == list(range(s_kv)), (s_kv, ns)
+            subs = [-(-(e - b) // 16) for b, e in ranges]
+            assert max(subs) - min(subs) <= 1, (s_kv, ns)
+            assert ranges[-1][1] == s_kv  # the last split holds the newest token
+
+
+@pytest.mark.parametrize("ns", [1, 5, 16])
+def test_fused_ranges_split_merge_matches_float64_decode(ns):
+    """The same split arithmetic on the fused boundaries: partials are the
+    softmax over their token ranges and the merge is the full attention."""
+    qg, kc, vc = _dec_case(13, 2, 4, 300)
+    pos = 260
+    att, lse = oracle.attn_decode_split(qg, kc, vc, qk_scale_f16_bits(), pos, 32, ns,
+                                        fused_ranges=True)
+    out = oracle.attn_decode_merge(att, lse, 4).astype(np.float32)
+    scale = float(np.array([qk_scale_f16_bits()], np.uint16).view(np.float16)[0])
+    ref = _attn_f64(qg.reshape(1, 8, D), kc, vc, scale, pos + 1, pos).reshape(2, 4, D)
+    assert np.max(np.abs(out - ref)) < 2e-3
+    for s in range(ns):
+        lo, hi = oracle.decode_split_range_fused(pos + 1, ns, s)
+        if lo >= hi:
+            assert np.all(lse[:, s * 4:s * 4 + 4] == np.float32(-1e30))
+            continue
+        for h in range(2):
+            logits = qg[h].astype(np.float64) @ kc[h, lo:hi].astype(np.float64).T * scale
+            p = np.exp(logits - logits.max(1, keepdims=True))
+            part = p / p.sum(1, keepdims=True) @ vc[h, lo:hi].astype(np.float64)
+            rows = slice(s * 4, s * 4 + 4)
+            assert np.max(np.abs(att[h, rows].astype(np.float64) - part)) < 2e-3
+            lse_ref = (np.log(np.exp(logits).sum(1))) / math.log(2)
+            assert np.max(np.abs(lse[h, rows] - lse_ref)) < 1e-4
+
+
 def test_empty_split_and_single_key():
     qg, kc, vc = _dec_case(11, 2, 4, 64)
     att, lse = oracle.attn_decode_split(qg, kc, vc, qk_scale_f16_bits(), 0, 32, 4)
