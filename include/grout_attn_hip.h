@@ -64,12 +64,12 @@ const char* grout_status_string(int32_t status);
 #define GROUT_MAX_DECODE_SPLITS 1024
 #define GROUT_MAX_PREFILL_SPLITS 1024
 
-/* --------------------------------------------------------- RoPE table (A1) */
+/* -------------------------------------------------------------- RoPE table */
 /* Replaces build_inv_freq (src/model.rs:5992-6003): host-side, f32,
  * out[j] = 1 / theta^((2j)/head_dim) for j < head_dim/2.  No device work. */
 int32_t grout_build_inv_freq(float theta, int32_t head_dim, float* out_host);
 
-/* ---------------------------------------- fused QK norm + RoPE + KV (A2) */
+/* --------------------------------------------- fused QK norm + RoPE + KV */
 /* Replaces qk_norm_rope_kv_prefill_raw_f16 (src/kernels.rs:3415-3732) as
  * launched by execute_qk_norm_rope_kv_prefill_op_ctx (src/model.rs:4463-4598).
  *   q [seq_len, num_q_heads, 128], k/v [seq_len, num_kv_heads, 128] f16;
@@ -89,7 +89,7 @@ int32_t grout_qk_norm_rope_kv_prefill(const uint16_t* q, const uint16_t* k, cons
                                       int32_t head_dim, int32_t max_seq_len,
                                       grout_stream_t stream);
 
-/* ---------------------------------------- fused decode variant (A3) */
+/* --------------------------------------------- fused decode variant */
 /* Replaces qk_norm_rope_kv_decode_raw_f16 (src/kernels.rs:3750-4016) as
  * recorded in the decode graph (src/model.rs:3194-3221).
  *   qkv = the QKV GEMV output [Q(num_q_heads*128) | K(num_kv_heads*128) |
@@ -128,7 +128,7 @@ int32_t grout_kv_cache_update_seq_dynpos(const uint16_t* new_k, const uint16_t* 
                                          int32_t num_kv_heads, int32_t head_dim,
                                          int32_t max_seq_len, grout_stream_t stream);
 
-/* ------------------------------------------ causal prefill attention (A4-A7) */
+/* -------------------------------------------------- causal prefill attention */
 /* Replaces fmha_prefill_causal / fmha_prefill_gqa / fmha_prefill_gqa_lpt /
  * flash_attn_causal_seq_f16 (src/kernels.rs:1037-1862) as dispatched by
  * attend_seq_arc_into_ctx_with_position (src/model.rs:5638-5834).
@@ -170,7 +170,7 @@ int32_t grout_attn_prefill_sched(const uint16_t* q, const uint16_t* k_cache,
                                  grout_stream_t stream);
 int64_t grout_attn_prefill_sched_counter_bytes(void);
 
-/* --------------------------------------------------- split-K prefill (A8) */
+/* -------------------------------------------------------- split-K prefill */
 /* Replaces fmha_prefill_gqa_lpt_split (src/kernels.rs:1872-2142), launched by
  * the attention microbench (benchmarks/src/bin/attention_microbench.rs:418-469)
  * with generics BM = block_m, BN = block_n, GROUP = group, NUM_KV_SPLITS =
@@ -211,7 +211,7 @@ int64_t grout_attn_prefill_split_partial_bytes(int32_t num_q_heads, int32_t head
 int64_t grout_attn_prefill_split_lse_bytes(int32_t num_q_heads, int32_t q_len, int32_t block_m,
                                            int32_t group, int32_t num_splits);
 
-/* ------------------------------------- decode-layer ops around attention (N1) */
+/* ------------------------------------------ decode-layer ops around attention */
 /* Replaces add_rms_norm_decode_raw_f16 (src/kernels.rs:3076-3216) as recorded
  * in the decode graph (src/model.rs:3151-3163, 3513-3526): for one row of n,
  * combined = f32(residual) + f32(x); inv = 1/sqrt(sum(combined^2)/n + eps);
@@ -254,7 +254,7 @@ int32_t grout_argmax_blocks(int32_t n);
 int32_t grout_argmax_f16(const uint16_t* logits, float* block_max, uint32_t* block_idx,
                          uint32_t* token, int32_t n, grout_stream_t stream);
 
-/* ------------------------------------------------ split-K GQA decode (A9) */
+/* ----------------------------------------------------- split-K GQA decode */
 /* Replaces fmha_decode_gqa_split (src/kernels.rs:2586-2749) as recorded at
  * src/model.rs:3428-3452.
  *   q [num_kv_heads, group, 128] f16 (first num_q_heads*128 of q_out);
@@ -276,7 +276,7 @@ int32_t grout_attn_decode_split(const uint16_t* q, const uint16_t* k_cache,
                                 int32_t group, int32_t head_dim, int32_t max_seq_len,
                                 int32_t block_n, int32_t num_splits, grout_stream_t stream);
 
-/* ------------------------------------------------------ split-K merge (A10) */
+/* ------------------------------------------------------------ split-K merge */
 /* Replaces splitk_reduce_merge (src/kernels.rs:2771-2868) as recorded at
  * src/model.rs:3453-3473:  w_s = 2^(lse_s - max) / max(sum 2^(lse_s - max), 1e-8),
  * out[kvh, g, :] = f16(sum_s w_s * att_partial[kvh, s*group+g, :]). */
@@ -284,7 +284,7 @@ int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_pa
                                 uint16_t* out, int32_t num_kv_heads, int32_t group,
                                 int32_t head_dim, int32_t num_splits, grout_stream_t stream);
 
-/* --------------------------------------- fused decode step (A3+A9+A10) */
+/* --------------------------------------------------- fused decode step */
 /* One launch doing what grout's decode graph records as three ops per layer
  * (src/model.rs:3194-3221, 3428-3473): RMSNorm + RoPE of the G query rows of
  * each KV head (q_out rows [0, num_q_heads) are written, as A3 does), the
@@ -354,7 +354,7 @@ int32_t grout_attn_decode_pick_splits(int32_t cu_count, int32_t num_kv_heads,
 /* Number of compute units of a device (hipDeviceAttributeMultiprocessorCount). */
 int32_t grout_device_cu_count(int32_t device, int32_t* cu_count);
 
-/* --------------------------------------------------- hipGraph helpers (A14) */
+/* --------------------------------------------------------- hipGraph helpers */
 /* Replace cuda-async's CudaGraph::scope / launch (src/model.rs:3118-3648,
  * :388-391).  begin/end wrap hipStreamBeginCapture / EndCapture +
  * hipGraphInstantiate on `stream` (thread-local capture mode). */
@@ -371,7 +371,7 @@ int32_t grout_graph_destroy(grout_graph* graph);
 int32_t grout_set_position_async(uint32_t* d_position, uint32_t position,
                                  grout_stream_t stream);
 
-/* ------------------------------------------- decode graph runner (A14) */
+/* ------------------------------------------------- decode graph runner */
 /* The attention slice of DecodeCudaGraphRunner (src/model.rs:318-493): one
  * hipGraph holding the fused decode step (grout_attn_decode_fused: QK
  * norm/RoPE/KV write, split-K decode, merge) for one layer's buffers,
@@ -427,7 +427,7 @@ int32_t grout_decode_runner_zero_kv(grout_decode_runner* runner);
  * then frees the graph. */
 int32_t grout_decode_runner_destroy(grout_decode_runner* runner);
 
-/* -------------------------------------- checkpoint formats (N4) */
+/* ------------------------------------------- checkpoint formats */
 /* Source element types of grout_cast_to_f16 (safetensors dtypes the
  * reference's loader accepts, src/loader.rs:109-145). */
 #define GROUT_DTYPE_F16 0
@@ -442,7 +442,7 @@ int32_t grout_decode_runner_destroy(grout_decode_runner* runner);
 int32_t grout_cast_to_f16(const void* src, int32_t src_dtype, uint16_t* dst, int64_t n,
                           grout_stream_t stream);
 
-/* ------------------------------------ Qwen3 decode token step (N1) */
+/* ----------------------------------------- Qwen3 decode token step */
 /* The whole decode graph of DecodeCudaGraphRunner (src/model.rs:3118-3648)
  * on this library's kernels: embedding + input RMSNorm of *token, then per
  * layer [add + input RMSNorm] -> qkv GEMV -> fused QK norm/RoPE/KV write +

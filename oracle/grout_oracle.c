@@ -627,7 +627,7 @@ void go_attn_prefill_split_merge(const uint16_t* att_partial, const float* lse_p
     free(w);
 }
 
-/* ------------------------------------------------- decode-layer ops (N1) -- */
+/* ------------------------------------------------------ decode-layer ops -- */
 
 /* src/kernels.rs:3076-3216 add_rms_norm_decode_raw_f16 (one row of n):
  * combined = f32(residual) + f32(x) (:3143-3146), ss = sum combined^2 (f32,
