@@ -179,10 +179,17 @@ constexpr int kPfRows = 32;
 // kDyn: persistent workgroups that claim tasks from the per-XCD queues above
 // instead of taking one task from blockIdx; each task runs exactly as in the
 // static grid, so the output is bit-identical.
-template <bool kSplit, bool kDyn>
-__global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(PrefillArgs a) {
+// kWaves = 4: group A alone (one wavefront per SIMD, no ping-pong partner), for
+// grids too small to fill the GPU: a tile step then takes one GEMM phase and
+// one softmax phase of one wavefront instead of two of each, which shortens
+// the latency of the heaviest workgroup.  Every wavefront computes exactly what
+// it computes in the 8-wavefront workgroup, so the output is bit-identical.
+template <bool kSplit, bool kDyn, int kWaves = kPfWaves>
+__global__ __launch_bounds__(kWaves * kWave, 1) void attn_prefill_kernel(PrefillArgs a) {
     static_assert(!(kSplit && kDyn), "the split-K form keeps the static grid");
-    constexpr int kDmaPerWave = 16 / kPfWaves;  // K blocks (and V blocks) per wavefront
+    static_assert(kWaves == kPfWaves || (kWaves == 4 && !kSplit && !kDyn),
+                  "the 4-wavefront form is the plain static grid only");
+    constexpr int kDmaPerWave = 16 / kWaves;  // K blocks (and V blocks) per wavefront
     __shared__ __attribute__((aligned(1024))) unsigned char pf_lds[kPfStages * kPfStageBytes];
 
     const int tid = threadIdx.x;
@@ -297,7 +304,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     }
     const int kvh = T / a.blocks_per_head;
     const int rblk = T % a.blocks_per_head;
-    const int u = rblk * kPfWaves + wave;
+    const int u = rblk * kWaves + wave;
     const bool task_ok = u < a.tasks_per_head;
     const int pt = a.n_pos_tiles - 1 - u / a.group;
     const int g = u % a.group;
@@ -305,7 +312,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     const int row0 = pt * kPfRows;
     const int pos0 = a.query_start + row0;
 
-    const int pt_max = a.n_pos_tiles - 1 - (rblk * kPfWaves) / a.group;
+    const int pt_max = a.n_pos_tiles - 1 - (rblk * kWaves) / a.group;
     const int blk_kv_end = min(a.kv_len, a.query_start + pt_max * kPfRows + kPfRows);
     int wave_kv_end = task_ok ? min(a.kv_len, pos0 + kPfRows) : 0;
     // Key range [lo, hi) of this wavefront (all keys unless split) and the
@@ -328,7 +335,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
         if (wave_kv_end <= key_lo) wave_kv_end = 0;  // empty range: no tile
         // The ranges grow with the q block, so the workgroup's union runs from
         // its lowest block's start to its highest block's end.
-        const int pt_min = max(0, a.n_pos_tiles - 1 - (rblk * kPfWaves + kPfWaves - 1) / a.group);
+        const int pt_min = max(0, a.n_pos_tiles - 1 - (rblk * kWaves + kWaves - 1) / a.group);
         int lo_min, hi_min, lo_max, hi_max;
         split_range(pt_min * kPfRows / a.block_m, lo_min, hi_min);
         split_range(pt_max * kPfRows / a.block_m, lo_max, hi_max);
@@ -422,7 +429,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     // after both groups are past GEMM(0).
     {
         uint4_t* vz = reinterpret_cast<uint4_t*>(pf_lds + (kPfStages - 1) * kPfStageBytes + kPfKBytes);
-        for (int i = tid; i < kPfVBytes / 16; i += kPfWaves * kWave) vz[i] = uint4_t{0u, 0u, 0u, 0u};
+        for (int i = tid; i < kPfVBytes / 16; i += kWaves * kWave) vz[i] = uint4_t{0u, 0u, 0u, 0u};
     }
 
     // Per-lane LDS read offsets.  K (A operand of S^T = K Q^T): key 32mb + l32,
@@ -583,7 +590,7 @@ __global__ __launch_bounds__(kPfWaves * kWave, 1) void attn_prefill_kernel(Prefi
     // start of the step.  Issued by all eight wavefronts right after the
     // barrier, the copies queue behind each other and hold up the GEMM phase
     // of group A (measured ~1% slower, bit-identical output).
-    if (grp == 0) {
+    if (kWaves == 4 || grp == 0) {
         for (int t = 0; t <= ntiles; ++t) {
             open_tile_step(t);
             gemm_phase(t);
@@ -713,6 +720,18 @@ static int32_t launch_prefill(PrefillArgs a, int num_kv_heads, hipStream_t strea
     a.blocks_per_head = (a.tasks_per_head + kPfWaves - 1) / kPfWaves;
     const int64_t blocks = static_cast<int64_t>(a.blocks_per_head) * num_kv_heads;
     if (blocks > 0x7fffffff) return GROUT_ERR_KV_LEN;
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return static_cast<int32_t>(e);
+    if (2 * blocks <= static_cast<int64_t>(cus)) {
+        // At most half the CUs busy: 4-wavefront workgroups, twice as many.
+        a.blocks_per_head = (a.tasks_per_head + 3) / 4;
+        const int64_t blocks4 = static_cast<int64_t>(a.blocks_per_head) * num_kv_heads;
+        hipLaunchKernelGGL((attn_prefill_kernel<false, false, 4>), dim3(static_cast<unsigned>(blocks4)),
+                           dim3(4 * kWave), 0, stream, a);
+        return launch_status();
+    }
     hipLaunchKernelGGL((attn_prefill_kernel<false, false>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kPfWaves * kWave), 0, stream, a);
     return launch_status();
@@ -736,7 +755,7 @@ static int32_t launch_prefill_sched(PrefillArgs a, int num_kv_heads, uint32_t* s
     a.sched = sched;
     a.n_wg = cus;
     a.num_kv_heads = num_kv_heads;
-    // The lightest quarter of each head's blocks goes to the shared pool.
+    // The lightest quarter of each head's blocks goes to the XCD light queues.
     a.pool_block0 = a.blocks_per_head - a.blocks_per_head / 4;
     hipLaunchKernelGGL((attn_prefill_kernel<false, true>), dim3(static_cast<unsigned>(cus)),
                        dim3(kPfWaves * kWave), 0, stream, a);

@@ -113,3 +113,30 @@ def test_prefill_long_sampled_rows(gpu, S):
                                   row_step=61)
     rows = np.arange(3, S, 61)
     assert_close_attn(out[rows], ref[rows], "prefill S=2048 sampled")
+
+
+@pytest.mark.parametrize("S,G,qs", [(1024, 4, 0), (700, 2, 300)])
+def test_small_grid_workgroup_shape_is_bit_identical(gpu, S, G, qs):
+    """Grids that fill at most half the CUs run 4-wavefront workgroups, larger
+    ones 8-wavefront workgroups; every wavefront computes the same thing in
+    both, so a problem and the same problem with more KV heads appended (which
+    pushes the grid past the threshold) agree bit for bit on the shared heads."""
+    import torch
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n_pos = -(-S // 32)
+    hkv_small = 2
+    while 2 * (-(-n_pos * G // 8)) * (hkv_small + 1) <= cus:
+        hkv_small += 1
+    hkv_big = 2 * hkv_small
+    assert 2 * (-(-n_pos * G // 8)) * hkv_small <= cus < 2 * (-(-n_pos * G // 8)) * hkv_big
+    print(f"[prefill 4/8 waves] S={S} G={G} Hkv {hkv_small} vs {hkv_big}", flush=True)
+    q, kc, vc = _case(400 + S, hkv_big * G, hkv_big, S, qs, qs + S)
+    small = _run(torch, np.ascontiguousarray(q[:, :hkv_small * G]), np.ascontiguousarray(kc[:hkv_small]),
+                 np.ascontiguousarray(vc[:hkv_small]), qs)
+    big = _run(torch, q, kc, vc, qs)
+    assert np.array_equal(small.view(np.uint16), big[:, :hkv_small * G].view(np.uint16))
+    ref = oracle.attn_prefill_f32(np.ascontiguousarray(q[:, :hkv_small * G]), kc[:hkv_small],
+                                  vc[:hkv_small], SCALE, kv_len=qs + S, query_start=qs,
+                                  row_step=37)
+    assert_close_attn(small[::37], ref[::37], "4-wavefront workgroups, sampled rows")
