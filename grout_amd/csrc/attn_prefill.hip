@@ -201,10 +201,23 @@ __global__ __launch_bounds__(kWaves * kWave, 1) void attn_prefill_kernel(Prefill
 
     // XCD-aware, longest-first task order: consecutive workgroup ids go to
     // different XCDs, so T groups all workgroups of a KV head on one XCD, and
-    // within a head the latest (heaviest) position tiles come first.
+    // within a head the latest (heaviest) position tiles come first.  With
+    // fewer than 8 KV heads a head spans hx = 8/Hkv XCDs, which take its blocks
+    // in turn (block i*hx + j on the head's j-th XCD): each XCD then gets the
+    // same mix of heavy and light blocks, not a contiguous (heavy or light) run.
     const int nb = gridDim.x;
     const int b = blockIdx.x;
-    int T = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    int T = b;
+    if (nb % 8 == 0) {
+        const int hkv = nb / a.blocks_per_head;
+        const int x = b % 8, i = b / 8;
+        if (hkv < 8 && 8 % hkv == 0) {
+            const int hx = 8 / hkv;
+            T = (x / hx) * a.blocks_per_head + i * hx + x % hx;
+        } else {
+            T = x * (nb / 8) + i;
+        }
+    }
 
     // Dynamic schedule state (wave 0 claims; the task goes to all waves
     // through LDS).  The claim on the own queue is issued one task ahead, after
