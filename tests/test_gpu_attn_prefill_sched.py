@@ -41,7 +41,8 @@ def _inputs(torch, seed, q_len, hq, hkv, ms, outliers=False):
     (6144, 32, 8, 1000, False),  # a chunk at query_start > 0
     (20000, 8, 1, 0, False),     # one KV head: seven XCDs steal every heavy and light task
     (12000, 12, 3, 0, True),     # three KV heads, G = 4, ragged last block
-], ids=["c3", "hkv4", "hkv16", "chunk", "hkv1", "hkv3"])
+    (6144, 24, 12, 0, False),    # twelve KV heads: queues 0-3 hold two heads, 4-7 one
+], ids=["c3", "hkv4", "hkv16", "chunk", "hkv1", "hkv3", "hkv12"])
 def test_sched_bit_identical_to_static(gpu, q_len, hq, hkv, qs, outliers):
     import torch
 
