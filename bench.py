@@ -21,6 +21,8 @@ fp16 dense MFMA peak, and decode attention GB/s as a fraction of HBM peak.
             (prefill_c3_steady_state): from idle the GPU's power management
             takes ~50 launches to settle, so the headline window (the
             contract's warmup count) includes that transient.
+  power   = board power and per-XCD shader clocks (amd-smi) while c3 and the
+            MFMA probe each run for 5 s (power_state).
 
 Kernel durations come from HIP events recorded on the launch stream, around a
 run of back-to-back launches divided by the count.  The CPU baseline is the
@@ -180,6 +182,111 @@ def bench_prefill_steady(torch, ga, pre, steps, sustain=200):
                                    sched_counters=pre["counters"])
     ms, _ = time_region(torch, fn, steps, sustain)
     return dict(ms=ms, tflops=pre["flops"] / (ms * 1e-3) / 1e12, sustain=sustain)
+
+
+AMD_SMI = "/opt/rocm/bin/amd-smi"
+
+
+def _smi_sample():
+    """(socket power W, [gfx clock MHz per XCD]) from one `amd-smi metric` query,
+    or None when the tool is missing or its output is not understood."""
+    import subprocess
+
+    try:
+        r = subprocess.run([AMD_SMI, "metric", "-p", "-c", "--json"], capture_output=True,
+                           text=True, timeout=20)
+        g = json.loads(r.stdout)["gpu_data"][0]
+        clocks = g["clock"]
+        gfx = [clocks[k]["clk"]["value"] for k in sorted(clocks) if k.startswith("gfx_")]
+        return float(g["power"]["socket_power"]["value"]), [float(x) for x in gfx]
+    except Exception:  # noqa: BLE001 - telemetry is optional
+        return None
+
+
+def bench_power_state(torch, ga, pre, seconds: float = 5.0):
+    """Board power and per-XCD shader clocks while the c3 prefill runs back to
+    back for `seconds`, then while the MFMA ceiling probe does, sampled with
+    amd-smi from a second thread (the readings refresh about once a second, so
+    only samples from the second half of each phase count).  Shows whether a
+    phase runs at the power limit and at which clock; the fp16 dense peak at
+    the measured mean clock is 256 CU x 4096 FLOP/clk x clock.  Returns None
+    when amd-smi is unavailable."""
+    import threading
+
+    if not os.path.exists(AMD_SMI) or _smi_sample() is None:
+        return None
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            s = _smi_sample()
+            if s is not None:
+                samples.append((time.time(), s))
+            stop.wait(0.2)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+
+    def phase(fn, per_call):
+        torch.cuda.synchronize()
+        t0 = time.time()
+        rates = []
+        while time.time() - t0 < seconds:
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            r = fn()
+            b.record()
+            b.synchronize()
+            rates.append((time.time(), r if r is not None else a.elapsed_time(b) / per_call))
+        t1 = time.time()
+        mid = t0 + 0.5 * (t1 - t0)
+        ss = [s for t, s in samples if mid <= t <= t1]
+        late = sorted(r for t, r in rates if t >= mid)
+        if not ss or not late:
+            return None
+        pw = sorted(p for p, _ in ss)
+        nx = len(ss[0][1])
+        clk = [sorted(c[i] for _, c in ss)[len(ss) // 2] for i in range(nx)]
+        return {"socket_power_w": pw[len(pw) // 2], "gfx_clock_mhz": clk,
+                "samples": len(ss), "median_rate": late[len(late) // 2]}
+
+    n = 20
+
+    def prefill_chunk():
+        for _ in range(n):
+            ga.attend_prefill(pre["q"], pre["kc"], pre["vc"], pre["out"], 0,
+                              sched_counters=pre["counters"])
+
+    try:
+        pf = phase(prefill_chunk, n)
+        pr = phase(lambda: bench_mfma_probe(torch, launches=8)["mix"], 1)
+        time.sleep(2.0)
+        idle = [s for t, s in samples if t >= time.time() - 1.0]
+    finally:
+        stop.set()
+        th.join()
+
+    def at_clock(clk):
+        return 256 * 4096 * (sum(clk) / len(clk)) * 1e6 / 1e12
+
+    out = {"seconds_per_phase": seconds, "tool": "amd-smi metric -p -c"}
+    if pf is not None:
+        ms = pf.pop("median_rate")
+        tf = pre["flops"] / (ms * 1e-3) / 1e12
+        pk = at_clock(pf["gfx_clock_mhz"])
+        pf.update({"ms_per_launch": round(ms, 4), "TFLOP/s": round(tf, 1),
+                   "fp16_dense_peak_at_clock": round(pk, 1), "frac_of_peak_at_clock": round(tf / pk, 4)})
+        out["prefill_c3"] = pf
+    if pr is not None:
+        mix = pr.pop("median_rate")
+        pk = at_clock(pr["gfx_clock_mhz"])
+        pr.update({"mix_TFLOP/s": round(mix, 1), "fp16_dense_peak_at_clock": round(pk, 1),
+                   "frac_of_peak_at_clock": round(mix / pk, 4)})
+        out["mfma_probe"] = pr
+    if idle:
+        out["after_2s_idle"] = {"socket_power_w": idle[-1][0], "gfx_clock_mhz": idle[-1][1]}
+    return out
 
 
 def bench_prefill_split(torch, ga, pre, steps, num_splits=4, block_m=128, block_n=64):
@@ -833,7 +940,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["all", "prefill", "prefill-split", "decode", "norm", "kv",
                                        "mfma-probe", "decode-layer", "token-step", "hbm-probe",
-                                       "c1", "c5", "decode-graph-step"],
+                                       "c1", "c5", "decode-graph-step", "power"],
                     default="all",
                     help="run one workload only (for profiling runs); prints no JSON line "
                          "(decode-graph-step prints the c4 graph step as one JSON line)")
@@ -916,6 +1023,10 @@ def main(argv=None) -> int:
             log(f"c5: prefill {c5['ms']:.2f} ms ({c5['tflops']:.1f} TFLOP/s); split-K "
                 f"{c5['split_ms']:.2f} + {c5['merge_ms']:.2f} ms; decode {c5['decode_us']:.2f} "
                 f"us/step")
+        elif args.only == "power":
+            pre = bench_prefill(torch, ga, args.steps, args.warmup, gen)
+            pw = bench_power_state(torch, ga, pre)
+            log(f"power state: {json.dumps(pw)}")
         elif args.only == "decode-graph-step":
             dec = bench_decode(torch, ga, 64, 8, 32768, args.decode_replays, 20, gen, 200,
                                graph_only=True)
@@ -993,6 +1104,17 @@ def main(argv=None) -> int:
     steady = bench_prefill_steady(torch, ga, pre, args.steps)
     log(f"prefill c3 after {steady['sustain']} untimed launches: {steady['ms']:.3f} ms/launch, "
         f"{steady['tflops']:.1f} TFLOP/s (headline window: {pre['ms']:.3f} ms)")
+    log("power and clocks: c3 prefill, then the MFMA probe ...")
+    pw = bench_power_state(torch, ga, pre)
+    if pw is None:
+        log("power and clocks: amd-smi unavailable")
+    else:
+        for k in ("prefill_c3", "mfma_probe"):
+            if k in pw:
+                e = pw[k]
+                log(f"{k}: {e['socket_power_w']:.0f} W, gfx clocks {min(e['gfx_clock_mhz']):.0f}-"
+                    f"{max(e['gfx_clock_mhz']):.0f} MHz, {e['frac_of_peak_at_clock']:.3f} of the "
+                    f"fp16 peak at that clock ({e['fp16_dense_peak_at_clock']:.0f} TFLOP/s)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -1153,6 +1275,10 @@ def main(argv=None) -> int:
             "ms_per_step": round(steady["ms"], 4), "TFLOP/s": round(steady["tflops"], 2),
             "frac_of_fp16_peak": round(steady["tflops"] / PEAK_TFLOPS_F16, 4),
             "untimed_launches_before": steady["sustain"], "steps": args.steps},
+        # Board power and shader clocks while c3 and the MFMA probe run for a few
+        # seconds each: both sit at the board's power limit, below the 2.4 GHz
+        # the nominal peak assumes.
+        "power_state": pw,
         "qk_norm_rope_c3": {"us": round(nrm["ms"] * 1e3, 2), "GB/s": round(nrm["gbs"], 1),
                             "frac_of_hbm_peak": round(nrm["gbs"] / PEAK_HBM_GBS, 4)},
         "kv_cache_update_c3": {"us": round(kvu["ms"] * 1e3, 2), "GB/s": round(kvu["gbs"], 1),
