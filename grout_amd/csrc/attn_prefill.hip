@@ -727,6 +727,206 @@ __global__ __launch_bounds__(kWaves * kWave, 1) void attn_prefill_kernel(Prefill
     }
 }
 
+// Short prefill: for a launch whose row blocks need at most kSpWaves key tiles
+// and whose (query head, 32-row block) pairs fit one workgroup per CU.  The
+// grid above would walk up to 8 tiles in sequence in its heaviest workgroup;
+// here one workgroup takes one (query head, row block), its 8 wavefronts take
+// one 64-key tile each, and the 8 online-softmax partials (m, l, O) meet in
+// LDS: the critical path is one tile and a merge.  Each wavefront computes
+// S^T = K Q^T with K straight from global memory (an A operand is 16
+// contiguous bytes of one key row) and O^T += V^T P^T with V copied into its
+// own LDS region (the transposing reads need it there), in the LDS layout and
+// lane mapping of the main kernel.  The merge follows the split-K reduction:
+// M = max_w m_w, out = f16(sum_w 2^(m_w-M) O_w / max(sum_w 2^(m_w-M) l_w, 1e-8)).
+// Keys outside a row's causal range are -inf (a wavefront whose tile holds no
+// key of a row keeps m = -1e30, l = 0, O = 0 for it: weight 0); tile 0 holds
+// key 0, which every row sees, so M is always a real score.
+constexpr int kSpWaves = 8;
+constexpr int kSpORow = 132;  // f32 per LDS row of a merge partial (16-lane groups hit distinct banks)
+constexpr int kSpOBytes = 32 * kSpORow * 4;
+static_assert(kSpOBytes + 256 <= kPfVBytes, "a wavefront's merge partial fits its V region");
+
+__global__ __launch_bounds__(kSpWaves * kWave, 1) void attn_prefill_short_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(1024))) unsigned char sp_lds[kSpWaves * kPfVBytes];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid % kWave;
+    const int l32 = lane & 31;
+    const int hl = lane >> 5;
+
+    // Heaviest row blocks first; the query heads of a row block are consecutive.
+    const int qh = static_cast<int>(blockIdx.x % a.num_q_heads);
+    const int pt = a.n_pos_tiles - 1 - static_cast<int>(blockIdx.x / a.num_q_heads);
+    const int kvh = qh / a.group;
+    const int row0 = pt * kPfRows;
+    const int pos0 = a.query_start + row0;
+    const int blk_kv_end = min(a.kv_len, pos0 + kPfRows);
+    const int ntiles = (blk_kv_end + kPfBN - 1) / kPfBN;  // <= kSpWaves (host check)
+
+    unsigned char* vw = sp_lds + wave * kPfVBytes;
+    float16_t o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+    float m_w = kPfNegBig, l_w = 0.0f;
+
+    if (wave < ntiles) {
+        const int n0 = wave * kPfBN;
+        const uint16_t* kh = a.k_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
+        const uint16_t* vh = a.v_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
+        // K operands: kop[mb][kk] = K[n0 + 32mb + l32][16kk + 8hl .. +8]; rows
+        // at or past blk_kv_end read the last valid row (masked below).
+        half8_t kop[2][8];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int key = min(n0 + 32 * mb + l32, blk_kv_end - 1);
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk)
+                kop[mb][kk] = load_half8(kh + static_cast<int64_t>(key) * kHeadDim + 16 * kk + 8 * hl);
+        }
+        // V tile into this wavefront's region (issued after the K loads, so
+        // waiting for K does not wait for V): copy r fills block r with rows
+        // n0 + r + 16j, j = lane/16, clamped like the K rows.
+        const uint32_t vw0 = static_cast<uint32_t>(
+            (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(vw)));
+        const bool clamp = n0 + kPfBN > blk_kv_end;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            int64_t row_base = static_cast<int64_t>(n0 + r) * kHeadDim;
+            uint32_t off = 4096u * static_cast<uint32_t>(lane >> 4) + 16u * (lane & 15);
+            if (clamp) {
+                const int row = min(n0 + r + 16 * (lane >> 4), blk_kv_end - 1);
+                row_base = static_cast<int64_t>(n0) * kHeadDim;
+                off = static_cast<uint32_t>(row - n0) * 256u + 16u * (lane & 15);
+            }
+            lds_dma16(vh + row_base, off, vw0 + kPfVBlock * r);
+        }
+        half8_t qop[8];
+        {
+            const int row = row0 + l32;
+            const bool ok = row < a.q_len;
+            const uint16_t* qr = a.q + (static_cast<int64_t>(ok ? row : 0) * a.num_q_heads + qh) * kHeadDim;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) qop[kk] = ok ? load_half8(qr + 16 * kk + 8 * hl) : half8_t{};
+        }
+        float16_t s[2];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[mb][r] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32x32x16(kop[mb][kk], qop[kk], s[mb]);
+        if (n0 + kPfBN - 1 > pos0 || n0 + kPfBN > a.kv_len) {
+            const int n_end = min(pos0 + l32 + 1, a.kv_len);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = n0 + 32 * mb + 8 * (r >> 2) + 4 * hl + (r & 3);
+                    if (key >= n_end) s[mb][r] = -__builtin_inff();
+                }
+        }
+        const float c = a.scale_log2;
+        float mx = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = (mb == 0 ? 2 : 0); r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[mb][r], s[mb][r + 1]));
+        mx = fmaxf(mx, swap_halves(mx));
+        m_w = fmaxf(kPfNegBig, mx * c);
+        half8_t pop[4];
+        float ps[4];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(s[mb][r], c, -m_w));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 1], c, -m_w));
+                const int k = (r >> 1) & 3;
+                ps[k] = (mb == 0 && r < 8) ? (p0 + p1) : ps[k] + (p0 + p1);
+                pop[2 * mb + (r >> 3)][r & 7] = static_cast<half_t>(p0);
+                pop[2 * mb + (r >> 3)][(r & 7) + 1] = static_cast<half_t>(p1);
+            }
+        l_w = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wavefront's V copies landed
+        asm volatile("" ::: "memory");
+        const int gi = lane >> 4, ii = lane & 15;
+        const unsigned char* vb = vw + (4 * (gi >> 1) + (ii >> 2)) * kPfVBlock + 32 * (gi & 1) + 8 * (ii & 3);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const unsigned char* p0 = vb + 256 * (i >> 2) + 64 * (i & 3);
+            const half8_t va = cat(lds_read_tr16(reinterpret_cast<const half_t*>(p0)),
+                                   lds_read_tr16(reinterpret_cast<const half_t*>(p0 + 8 * kPfVBlock)));
+            o[i & 3] = mfma32x32x16(va, pop[i >> 2], o[i & 3]);
+        }
+    }
+
+    // Every wavefront's partial into its own region (its V reads are done
+    // after the barrier), rows of kSpORow f32, then m and the row sum l.
+    pf_barrier();
+    {
+        float* orow = reinterpret_cast<float*>(vw) + l32 * kSpORow;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4_t v = {o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]};
+                *reinterpret_cast<float4_t*>(orow + 32 * db + 8 * j + 4 * hl) = v;
+            }
+        const float lt = l_w + swap_halves(l_w);
+        float* ml = reinterpret_cast<float*>(vw + kSpOBytes);
+        if (hl == 0) {
+            ml[l32] = m_w;
+            ml[32 + l32] = lt;
+        }
+    }
+    pf_barrier();
+    // Thread (row, 8 dims): the 8 partials of its row.
+    const int row = tid >> 4, d8 = tid & 15;
+    float mw[kSpWaves];
+    float M = kPfNegBig;
+#pragma unroll
+    for (int w = 0; w < kSpWaves; ++w) {
+        mw[w] = reinterpret_cast<const float*>(sp_lds + w * kPfVBytes + kSpOBytes)[row];
+        M = fmaxf(M, mw[w]);
+    }
+    float L = 0.0f;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < kSpWaves; ++w) {
+        const float wt = __builtin_amdgcn_exp2f(mw[w] - M);
+        const float* base = reinterpret_cast<const float*>(sp_lds + w * kPfVBytes);
+        L += wt * base[kSpOBytes / 4 + 32 + row];
+        const float4_t x0 = *reinterpret_cast<const float4_t*>(base + row * kSpORow + 8 * d8);
+        const float4_t x1 = *reinterpret_cast<const float4_t*>(base + row * kSpORow + 8 * d8 + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc[e] += wt * x0[e];
+            acc[4 + e] += wt * x1[e];
+        }
+    }
+    const double rl = 1.0 / static_cast<double>(fmaxf(L, 1.0e-8f));
+    half8_t h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = div_to_half(acc[e], rl);
+    if (row0 + row < a.q_len)
+        store_half8(a.out + (static_cast<int64_t>(row0 + row) * a.num_q_heads + qh) * kHeadDim + 8 * d8, h);
+}
+
+// The short form applies when every row block needs at most kSpWaves key
+// tiles and the (query head, row block) pairs number at most one per CU.
+// (The last row block's key range ends at min(kv_len, query_start + 32 *
+// row blocks), as the kernel computes it.)
+static bool prefill_short_fits(const PrefillArgs& a, int cus) {
+    const int64_t n_blocks = (static_cast<int64_t>(a.q_len) + kPfRows - 1) / kPfRows;
+    const int64_t last_end = min(static_cast<int64_t>(a.kv_len),
+                                 static_cast<int64_t>(a.query_start) + kPfRows * n_blocks);
+    return last_end <= static_cast<int64_t>(kSpWaves) * kPfBN && n_blocks * a.num_q_heads <= cus;
+}
+
 static int32_t launch_prefill(PrefillArgs a, int num_kv_heads, hipStream_t stream) {
     a.n_pos_tiles = (a.q_len + kPfRows - 1) / kPfRows;
     a.tasks_per_head = a.n_pos_tiles * a.group;
@@ -737,6 +937,12 @@ static int32_t launch_prefill(PrefillArgs a, int num_kv_heads, hipStream_t strea
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return static_cast<int32_t>(e);
+    if (prefill_short_fits(a, cus)) {
+        const int64_t sblocks = static_cast<int64_t>(a.n_pos_tiles) * a.num_q_heads;
+        hipLaunchKernelGGL(attn_prefill_short_kernel, dim3(static_cast<unsigned>(sblocks)),
+                           dim3(kSpWaves * kWave), 0, stream, a);
+        return launch_status();
+    }
     if (2 * blocks <= static_cast<int64_t>(cus)) {
         // At most half the CUs busy: 4-wavefront workgroups, twice as many.
         a.blocks_per_head = (a.tasks_per_head + 3) / 4;

@@ -140,3 +140,53 @@ def test_small_grid_workgroup_shape_is_bit_identical(gpu, S, G, qs):
                                   vc[:hkv_small], SCALE, kv_len=qs + S, query_start=qs,
                                   row_step=37)
     assert_close_attn(small[::37], ref[::37], "4-wavefront workgroups, sampled rows")
+
+
+def _short_form_applies(cus, hq, S, qs, kv_len):
+    """The host rule of the short form: every 32-row block needs at most 8 key
+    tiles of 64, and one workgroup per (query head, row block) fits the CUs."""
+    n_blocks = -(-S // 32)
+    return min(kv_len, qs + 32 * n_blocks) <= 8 * 64 and n_blocks * hq <= cus
+
+
+@pytest.mark.parametrize("hq,hkv,S,qs,MS,kv_len,seed", [
+    (16, 8, 50, 40, 96, None, 11),    # rows 40..63's second tile holds none of their keys
+    (8, 2, 512, 0, 512, None, 12),    # 8 key tiles in the last row block, G = 4
+    (32, 8, 256, 0, 256, None, 13),   # 256 workgroups: one per CU on MI355X
+    (4, 1, 300, 200, 512, 480, 14),   # kv_len short of query_start + q_len (rows past it see 480 keys)
+    (21, 7, 321, 7, 400, None, 15),   # ragged: a partial last row block, G = 3
+])
+def test_short_prefill_matches_oracle(gpu, hq, hkv, S, qs, MS, kv_len, seed):
+    """Launches small enough for the short form (one workgroup per query head
+    and 32-row block, one key tile per wavefront, partials merged in LDS)."""
+    import torch
+
+    kv = qs + S if kv_len is None else kv_len
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert _short_form_applies(cus, hq, S, qs, kv), "shape outside the short form"
+    print(f"[short prefill] hq={hq} hkv={hkv} S={S} qs={qs} kv_len={kv}", flush=True)
+    q, kc, vc = _case(seed, hq, hkv, S, qs, MS)
+    out = _run(torch, q, kc, vc, qs, kv_len=kv)
+    ref = oracle.attn_prefill_f32(q, kc, vc, SCALE, kv_len=kv, query_start=qs)
+    assert_close_attn(out, ref, f"short prefill hq={hq} hkv={hkv} S={S} qs={qs} kv_len={kv}")
+
+
+def test_short_prefill_boundary_agrees_with_grid(gpu):
+    """The same problem on both sides of the short form's CU rule: the short
+    launch and the grid launch (one more query head pushes the grid past one
+    workgroup per CU) agree within the attention tolerance on the shared heads."""
+    import torch
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    S, G = 256, 2
+    hq_short = (cus // (S // 32)) // G * G
+    hq_grid = hq_short + G
+    assert _short_form_applies(cus, hq_short, S, 0, S) and not _short_form_applies(cus, hq_grid, S, 0, S)
+    print(f"[short prefill boundary] hq {hq_short} vs {hq_grid}", flush=True)
+    q, kc, vc = _case(16, hq_grid, hq_grid // G, S, 0, S)
+    short = _run(torch, np.ascontiguousarray(q[:, :hq_short]), np.ascontiguousarray(kc[:hq_short // G]),
+                 np.ascontiguousarray(vc[:hq_short // G]), 0)
+    grid = _run(torch, q, kc, vc, 0)
+    assert_close_attn(short, grid[:, :hq_short].astype(np.float32), "short vs grid")
+    ref = oracle.attn_prefill_f32(q, kc, vc, SCALE, kv_len=S, query_start=0, row_step=13)
+    assert_close_attn(grid[::13], ref[::13], "grid, sampled rows")
