@@ -35,6 +35,9 @@
 //  * Heavy (late-position) workgroups launch first (longest-processing-time
 //    order) and all workgroups of one KV head go to one XCD so its K/V stay
 //    in that XCD's L2.
+//  * Small launches (row blocks of at most 8 key tiles, one workgroup per
+//    query head and row block within the CU count) take a short form: the 8
+//    wavefronts of a workgroup take one key tile each and merge in LDS.
 #include <math.h>
 
 #include <type_traits>

@@ -140,7 +140,12 @@ int32_t grout_kv_cache_update_seq_dynpos(const uint16_t* new_k, const uint16_t* 
  * Query row m sits at position query_start+m and attends keys
  * n < min(kv_len, query_start+m+1); kv_head = q_head / (num_q_heads/num_kv_heads).
  * Softmax in base 2 with qk_scale/ln2 folded in, f32 accumulation, P rounded
- * to f16 for the PV product, out = f16(acc / max(l, 1e-8)). */
+ * to f16 for the PV product, out = f16(acc / max(l, 1e-8)).
+ * Small launches (every 32-row block needs at most 512 keys, and query heads x
+ * row blocks is at most the CU count) split each row block's keys across the
+ * wavefronts of one workgroup and merge the partials on chip: the same math,
+ * rounded in another order (within the attention tolerance, not bit-identical
+ * to the grid form). */
 int32_t grout_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                            uint16_t* out, float qk_scale, int32_t num_q_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t q_len,
