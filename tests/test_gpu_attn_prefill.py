@@ -155,6 +155,8 @@ def _short_form_applies(cus, hq, S, qs, kv_len):
     (32, 8, 256, 0, 256, None, 13),   # 256 workgroups: one per CU on MI355X
     (4, 1, 300, 200, 512, 480, 14),   # kv_len short of query_start + q_len (rows past it see 480 keys)
     (21, 7, 321, 7, 400, None, 15),   # ragged: a partial last row block, G = 3
+    (16, 8, 1, 511, 512, None, 17),   # one row over 512 keys: every wavefront holds a tile
+    (8, 4, 32, 480, 512, None, 18),   # one full row block at the end of the range
 ])
 def test_short_prefill_matches_oracle(gpu, hq, hkv, S, qs, MS, kv_len, seed):
     """Launches small enough for the short form (one workgroup per query head
