@@ -41,6 +41,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "abi_util.h"
 #include "common.h"
@@ -169,6 +170,24 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// Max / sum over each 32-lane half of the wavefront, every lane of the half
+// ending with the same value: DPP quad swaps (lane ^ 1, ^ 2), the 8-lane and
+// 16-lane mirrors, then v_permlane16_swap (lane ^ 16).  Each step pairs
+// lanes that already hold equal values, so the sum is the same float in
+// every lane of the half.
+template <typename Op>
+__device__ __forceinline__ float half32_reduce(float x, Op op) {
+    auto dpp = [](float v, auto ctrl) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                     decltype(ctrl)::value, 0xf, 0xf, false));
+    };
+    x = op(x, dpp(x, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+    x = op(x, dpp(x, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+    x = op(x, dpp(x, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+    x = op(x, dpp(x, std::integral_constant<int, 0x140>{}));  // row_mirror
+    return op(x, swap_rows16(x));
+}
+
 // RMSNorm + RoPE of one 128-wide row held by 8 lanes (lane t: elements
 // [8t,8t+8) and [64+8t, 64+8t+8)), same operation order as
 // qk_norm_rope_kv_kernel.
@@ -227,6 +246,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     __shared__ float s_cos[64], s_sin[64];
     __shared__ uint32_t s_flag;
     __shared__ uint32_t s_next_sub;  // next sub-chunk of the split not yet taken by a wavefront
+    __shared__ float s_wsum[GROUT_MAX_DECODE_GROUP];  // merge: sum of the split weights per query row
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -649,10 +669,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         const float* lse_h = a.lse_partial + static_cast<int64_t>(kvh) * NS * G;
         const unsigned char* rows_l = lds;
         float* lse_t = reinterpret_cast<float*>(lds + kMergeRows * 256);
-        float m_i[2] = {-INFINITY, -INFINITY}, s_i[2] = {0.0f, 0.0f};
-        float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        for (int s0 = 0; s0 < NS; s0 += SB) {
-            const int ns_b = min(SB, NS - s0);
+        // One batch of up to kMergeRows partial rows: rows into the stages,
+        // LSEs into the [g][split] table (padded with -1e30 to SBp).
+        auto load_batch = [&](int s0, int ns_b) {
             const int rows = ns_b * G;
             const uint16_t* src = part_h + static_cast<int64_t>(s0) * G * kHeadDim;
             // Copy i moves rows 4i..4i+3 (lane l: row 4i + l/16, 16-byte chunk
@@ -672,6 +691,77 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             }
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
             lds_barrier();
+        };
+        if (NS <= SB && NS <= 64) {
+            // All splits in one batch: the weights w_s = 2^(lse_s - M) of a
+            // query row are computed once, by one 32-lane half per row (split
+            // s at lane s%32, s/32 its slot), and replace the LSEs in the table;
+            // then each thread sums its 4 dims over the splits.
+            load_batch(0, NS);
+            for (int gi = tid >> 5; gi < G; gi += kDecThreads / 32) {
+                const int l = tid & 31;
+                float* lrow = lse_t + gi * SBp;
+                const float v0 = lrow[l];
+                const float v1 = NS > 32 ? lrow[32 + l] : kNegBig;
+                const float mx = half32_reduce(fmaxf(v0, v1), [](float x, float y) { return fmaxf(x, y); });
+                const float w0 = __builtin_amdgcn_exp2f(v0 - mx);
+                const float w1 = NS > 32 ? __builtin_amdgcn_exp2f(v1 - mx) : 0.0f;
+                const float sw = half32_reduce(w0 + w1, [](float x, float y) { return x + y; });
+                lrow[l] = w0;
+                if (NS > 32) lrow[32 + l] = w1;
+                if (l == 0) s_wsum[gi] = sw;
+            }
+            lds_barrier();
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int it = tid + kDecThreads * k;
+                if (it < G * 32) {
+                    const int g = it >> 5, c = it & 31;
+                    const float* wrow = lse_t + g * SBp;
+                    const unsigned char* rbase = rows_l + g * 256 + 8 * c;
+                    float acc4[4] = {0.f, 0.f, 0.f, 0.f};
+                    for (int sc = 0; sc < NS; sc += 32) {
+                        if (NS - sc >= 32) {
+                            const unsigned char* xb = rbase + sc * G * 256;
+                            const int xstride = G * 256;
+                            half4_t xs[32];
+#pragma unroll
+                            for (int u = 0; u < 32; ++u)
+                                xs[u] = *reinterpret_cast<const half4_t*>(xb + u * xstride);
+                            float wv[32];
+#pragma unroll
+                            for (int u = 0; u < 8; ++u) {
+                                const float4_t w4 = *reinterpret_cast<const float4_t*>(wrow + sc + 4 * u);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) wv[4 * u + e] = w4[e];
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                            for (int u = 0; u < 32; ++u)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc4[e] += wv[u] * static_cast<float>(xs[u][e]);
+                        } else {
+                            for (int u = sc; u < NS; ++u) {
+                                const float w = wrow[u];
+                                const half4_t x = *reinterpret_cast<const half4_t*>(rbase + u * G * 256);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc4[e] += w * static_cast<float>(x[e]);
+                            }
+                        }
+                    }
+                    const float inv = 1.0f / fmaxf(s_wsum[g], 1.0e-8f);
+                    half4_t h;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) h[e] = static_cast<half_t>(acc4[e] * inv);
+                    *reinterpret_cast<half4_t*>(a.out + (static_cast<int64_t>(kvh) * G + g) * kHeadDim + 4 * c) = h;
+                }
+            }
+        } else {
+        float m_i[2] = {-INFINITY, -INFINITY}, s_i[2] = {0.0f, 0.0f};
+        float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        for (int s0 = 0; s0 < NS; s0 += SB) {
+            const int ns_b = min(SB, NS - s0);
+            load_batch(s0, ns_b);
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 const int it = tid + kDecThreads * k;
@@ -740,6 +830,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
                 *reinterpret_cast<half4_t*>(a.out + (static_cast<int64_t>(kvh) * G + g) * kHeadDim + 4 * c) = h;
             }
         }
+        }  // batched merge
         if (tid == 0 && head_ticket == static_cast<uint32_t>(a.num_kv_heads) - 1u) {
             __hip_atomic_store(&a.counters[a.num_kv_heads * kDecCounterStride], 0u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
