@@ -224,6 +224,8 @@ def _fused_case(seed, hq, hkv, MS):
     (64, 4, 3000, 3100, 40, 77),   # G = 16: batches of 28 (28 + 12)
     (48, 4, 4000, 4100, 75, 78),   # G = 12: batches of 37 (37 + 37 + 1)
     (64, 4, 5000, 5100, 64, 79),   # G = 16: 28 + 28 + 8
+    (64, 8, 3000, 3100, 48, 80),   # G = 8, one batch of 48: two weight slots per lane
+    (64, 4, 2500, 2600, 20, 81),   # G = 16, one batch of 20: two passes of the weight rows
 ])
 def test_fused_step_matches_oracle(gpu, hq, hkv, pos, MS, ns, seed):
     """grout_attn_decode_fused = norm/RoPE/KV write + split + merge of the oracle;
