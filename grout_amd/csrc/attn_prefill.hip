@@ -788,9 +788,10 @@ __global__ __launch_bounds__(kSpWaves * kWave, 1) void attn_prefill_short_kernel
             for (int kk = 0; kk < 8; ++kk)
                 kop[mb][kk] = load_half8(kh + static_cast<int64_t>(key) * kHeadDim + 16 * kk + 8 * hl);
         }
-        // V tile into this wavefront's region (issued after the K loads, so
-        // waiting for K does not wait for V): copy r fills block r with rows
-        // n0 + r + 16j, j = lane/16, clamped like the K rows.
+        // V tile into this wavefront's region: copy r fills block r with rows
+        // n0 + r + 16j, j = lane/16, clamped like the K rows.  K, V and Q are
+        // in flight together (vector-memory ops retire in order, so the first
+        // MFMA's wait covers all three): one memory round trip for the tile.
         const uint32_t vw0 = static_cast<uint32_t>(
             (uintptr_t)((__attribute__((address_space(3))) unsigned char*)(vw)));
         const bool clamp = n0 + kPfBN > blk_kv_end;
