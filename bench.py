@@ -862,16 +862,16 @@ def cpu_baselines(torch, pre, dec, c5, c1):
 
     threads, visible = host_threads()
     res = {"threads": threads, "host_cpus_visible": visible}
-    # c3 prefill: rows 0::2 on all threads, rows 0::32 on one.
+    # c3 prefill: every row on all threads; rows 0::32 on one.
     q = pre["q"].cpu().numpy()
     kc = pre["kc"].cpu().numpy()
     vc = pre["vc"].cpu().numpy()
     S, hq = pre["S"], pre["hq"]
-    r_all, t_all, n_all = _cpu_prefill_rate(q, kc, vc, S, hq, 0, S, 2, threads)
+    r_all, t_all, n_all = _cpu_prefill_rate(q, kc, vc, S, hq, 0, S, 1, threads)
     r_one, t_one, n_one = _cpu_prefill_rate(q, kc, vc, S, hq, 0, S, 32, 1)
     res["c3"] = dict(value=r_all, unit="TFLOP/s", cores=threads, single_thread_value=r_one,
-                     sample=f"c3 inputs, query rows 0::2 ({n_all} of {S}) x {hq} heads on "
-                            f"{threads} threads ({t_all:.1f} s); rows 0::32 ({n_one}) on 1 "
+                     sample=f"c3 in full: all {n_all} query rows x {hq} heads on {threads} "
+                            f"threads ({t_all:.1f} s); rows 0::32 ({n_one} of {S}) on 1 "
                             f"thread ({t_one:.1f} s)")
     del q, kc, vc
     # c1 in full (norm output as the attention input), all threads and 1.

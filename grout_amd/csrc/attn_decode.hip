@@ -245,7 +245,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     __shared__ __attribute__((aligned(16))) half_t q_lds[GROUT_MAX_DECODE_GROUP * kHeadDim];
     __shared__ float s_cos[64], s_sin[64];
     __shared__ uint32_t s_flag;
-    __shared__ uint32_t s_next_sub;  // next sub-chunk of the split not yet taken by a wavefront
     __shared__ float s_wsum[GROUT_MAX_DECODE_GROUP];  // merge: sum of the split weights per query row
 
     const int split = blockIdx.x;
@@ -319,13 +318,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         tok_end = (tb < te) ? min(te * a.block_n, s_kv) : tok_begin;
     }
     const int nsub = (tok_end - tok_begin + kDecSubTok - 1) / kDecSubTok;
-    // The first kDecWaveStages sub-chunks of each wavefront are fixed
-    // (w, w+4, w+8, w+12); after that a wavefront takes the next untaken
-    // sub-chunk from an LDS counter whenever a stage of its ring frees, so
-    // the four wavefronts finish within about one sub-chunk of each other.
+    // Wavefront w owns sub-chunks w, w+4, w+8, ... of the split (its k-th is
+    // w + 4k): a fixed assignment, so every launch accumulates the same
+    // tokens in the same order and the output is bit-reproducible.
     const int nk = nsub > wave ? (nsub - wave + kDecWaves - 1) / kDecWaves : 0;
     const int n_first = min(kDecWaveStages, nk);
-    if (tid == 0) s_next_sub = kDecWaves * kDecWaveStages;
 
     const uint16_t* kh = a.k_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
     const uint16_t* vh = a.v_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
@@ -467,15 +464,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             v_off[db] = kDecSubBytes + tr * 256 + 16 * ((2 * db + ((n & 3) >> 1)) ^ dec_swz(tr)) + 8 * (n & 1);
     }
 
-    // Sub-chunks in this wavefront's stages k%4 .. (k+3)%4: q0 (the current
-    // one) .. q3; n_issued counts the sub-chunks it has issued so far.
-    int q0 = wave, q1 = wave + kDecWaves, q2 = wave + 2 * kDecWaves, q3 = wave + 3 * kDecWaves;
-    int n_issued = n_first;
-    bool more = n_first == kDecWaveStages;  // untaken sub-chunks may remain
-    for (int k = 0; k < n_issued; ++k) {
+    for (int k = 0; k < nk; ++k) {
         // Sub-chunk k has landed once only the copies of this wavefront's later
         // sub-chunks (8 each, up to three) are outstanding.
-        const int younger = min(kDecWaveStages - 1, n_issued - 1 - k);
+        const int younger = min(kDecWaveStages - 1, nk - 1 - k);
         if (younger >= 3) {
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(24));
         } else if (younger == 2) {
@@ -485,8 +477,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         } else {
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
         }
+        const int cur = wave + kDecWaves * k;
         unsigned char* kb = lds + wave * kDecWaveBytes + (k % kDecWaveStages) * 2 * kDecSubBytes;
-        if (q0 == sub_pos) {
+        if (cur == sub_pos) {
             // The copy read the cache before the new row was stored: lanes
             // 0-15 put the rotated K row, lanes 16-31 the V row into row
             // tr_pos (swizzled).  A wavefront's LDS accesses complete in order.
@@ -507,25 +500,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         for (int cc = 0; cc < 4; ++cc) ka[cc] = *reinterpret_cast<const half8_t*>(kb + k_off[cc]);
 #pragma unroll
         for (int db = 0; db < 8; ++db) va[db] = lds_read_tr16(reinterpret_cast<const half_t*>(kb + v_off[db]));
-        const int cur = q0;
-        int next = -1;
-        if (more) {
-            uint32_t got = 0;
-            if (lane == 0) got = __hip_atomic_fetch_add(&s_next_sub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            next = __builtin_amdgcn_readfirstlane(static_cast<int>(got));
-            if (next < nsub) {
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                issue_sub(k + kDecWaveStages, next);
-                ++n_issued;
-            } else {
-                next = -1;
-                more = false;
-            }
+        if (k + kDecWaveStages < nk) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue_sub(k + kDecWaveStages, cur + kDecWaves * kDecWaveStages);
         }
-        q0 = q1;
-        q1 = q2;
-        q2 = q3;
-        q3 = next;
 
         const int t = tok_begin + kDecSubTok * cur;  // first token
         // S^T[token, head]: lane holds head n, tokens t + 4qgrp + r.
@@ -1039,19 +1017,17 @@ static_assert(kNoAllocCounterBytes ==
               "one counter line per KV head plus the head counter");
 static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 
-__global__ void zero_u32_kernel(uint32_t* p, int n) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
-}
-
 namespace {
 
 // Per-device address of `scratch` (the name is only a host-side stand-in):
-// looked up once per device with that device current, then used for every
-// kernel argument.
+// looked up with that device current, then used for every kernel argument.
+// A device counts as set up only once the lookup has succeeded, so a failed
+// set-up is tried again by the next call.  Nothing is written to the array
+// at set-up: static device storage is zero when the code object is loaded,
+// and every launch leaves the merge counters zero again.
 struct NoAllocDevice {
-    std::once_flag once;
-    unsigned char* ptr = nullptr;
-    int32_t status = GROUT_OK;
+    std::mutex mu;
+    unsigned char* ptr = nullptr;  // non-null once set up
 };
 constexpr int kNoAllocMaxDevices = 64;
 NoAllocDevice g_noalloc[kNoAllocMaxDevices];
@@ -1077,25 +1053,27 @@ extern "C" int32_t grout_attn_decode_fused_noalloc(
     if (e != hipSuccess) return static_cast<int32_t>(e);
     GROUT_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices, GROUT_ERR_SCRATCH);
     NoAllocDevice& d = g_noalloc[dev];
-    // Set-up, once per device: the array's address on this device, and its
-    // counters cleared in stream order (every launch leaves them zero again).
-    std::call_once(d.once, [&] {
-        void* p = nullptr;
-        const hipError_t ge = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (ge != hipSuccess) {
-            d.status = static_cast<int32_t>(ge);
-            return;
+    unsigned char* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(d.mu);
+        if (d.ptr == nullptr) {
+            // The first call on a device must not run under stream capture:
+            // the symbol lookup is not a stream operation and has no place
+            // in a graph.  The caller makes one call before capturing.
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            e = hipStreamIsCapturing(to_hip(stream), &cs);
+            if (e != hipSuccess) return static_cast<int32_t>(e);
+            if (cs != hipStreamCaptureStatusNone) return GROUT_ERR_GRAPH;
+            void* p = nullptr;
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return static_cast<int32_t>(e);
+            d.ptr = static_cast<unsigned char*>(p);
         }
-        d.ptr = static_cast<unsigned char*>(p);
-        constexpr int n = static_cast<int>(kNoAllocCounterBytes / 4);
-        hipLaunchKernelGGL(zero_u32_kernel, dim3(16), dim3(256), 0, to_hip(stream),
-                           reinterpret_cast<uint32_t*>(d.ptr), n);
-        d.status = launch_status();
-    });
-    if (d.status != GROUT_OK) return d.status;
-    uint32_t* counters = reinterpret_cast<uint32_t*>(d.ptr);
-    float* lse = reinterpret_cast<float*>(d.ptr + kNoAllocCounterBytes);
-    uint16_t* att = reinterpret_cast<uint16_t*>(d.ptr + kNoAllocCounterBytes + lse_bytes);
+        base = d.ptr;
+    }
+    uint32_t* counters = reinterpret_cast<uint32_t*>(base);
+    float* lse = reinterpret_cast<float*>(base + kNoAllocCounterBytes);
+    uint16_t* att = reinterpret_cast<uint16_t*>(base + kNoAllocCounterBytes + lse_bytes);
     return fused_decode(qkv, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache, att, lse, out,
                         counters, d_position, eps, qk_scale_f16, num_q_heads, num_kv_heads,
                         head_dim, max_seq_len, block_n, num_splits, advance_position, stream);

@@ -328,10 +328,13 @@ int64_t grout_attn_decode_counter_bytes(int32_t num_kv_heads);
  * 64 KiB of merge counters, then num_q_heads * num_splits LSEs (f32) and
  * partial rows (256 B).  Calls needing more, or num_kv_heads above
  * GROUT_NOALLOC_MAX_KV_HEADS, return GROUT_ERR_SCRATCH.  Nothing is
- * allocated; the first call on a device looks up the array's address and
- * clears its counters in stream order, and every launch leaves them zero.
- * All calls on one GPU share the array: calls that overlap on one GPU (two
- * streams, two threads) race. */
+ * allocated.  The first successful call on a device looks up the array's
+ * address (no stream work: the array is zero when the library is loaded,
+ * and every launch leaves its counters zero); that first call must not be
+ * made on a stream under capture, and returns GROUT_ERR_GRAPH if it is, so a
+ * caller makes one call before capturing.  A failed look-up is retried by
+ * the next call.  All calls on one GPU share the array: calls that overlap
+ * on one GPU (two streams, two threads) race. */
 #define GROUT_NOALLOC_SCRATCH_BYTES 4194304 /* 4 MiB */
 #define GROUT_NOALLOC_MAX_KV_HEADS 255
 int32_t grout_attn_decode_fused_noalloc(const uint16_t* qkv, const uint16_t* q_weight,

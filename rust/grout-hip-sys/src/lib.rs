@@ -17,10 +17,14 @@
 //!
 //! Calling rules (from the header): every function returns a status
 //! (0 = ok, < 0 = argument validation, > 0 = `hipError_t`); pointers are
-//! borrowed device memory; nothing allocates or synchronises the host, so
-//! the decode entry points can be captured into a hipGraph.  [`check`] turns
-//! a status into a `Result` whose error converts into `anyhow::Error` at
-//! grout's `?` sites.
+//! borrowed device memory.  The kernel entry points (`grout_qk_norm_rope_*`,
+//! `grout_attn_*`, `grout_kv_cache_*`, the decode-layer ops) allocate nothing
+//! and never synchronise the host, so the decode ones can be captured into a
+//! hipGraph.  The runners are set-up objects and do block: `*_create`
+//! allocates, captures and synchronises, `*_destroy` synchronises its
+//! stream, and a step that returns a token (`token_out`) waits for it.
+//! [`check`] turns a status into a `Result` whose error converts into
+//! `anyhow::Error` at grout's `?` sites.
 //!
 //! Not compiled in this repository (its build image has no Rust toolchain);
 //! `tests/test_rust_binding.py` checks the declarations below against the C

@@ -4,6 +4,8 @@ Small shapes (Hq=4, Hkv=2, D=128) with seeded N(0,1) inputs; f16 tensors are
 stored as their uint16 bit patterns, f32 as float32, in one .npz per op.
 Run from the repository root:  python tests/golden/make_golden.py
 """
+import hashlib
+import json
 import math
 import os
 import sys
@@ -82,7 +84,38 @@ def main():
         dec[f"nks{ns}_lse"] = lse
         dec[f"nks{ns}_out"] = bits(oracle.attn_decode_merge(att, lse, hq // hkv))
     np.savez_compressed(os.path.join(OUT, "attn_decode.npz"), **dec)
+
+    # Config c1 (Qwen3-0.6B layer, S=512 at positions 0..511, 16 Q / 8 KV
+    # heads, cache of 512 slots): SHA-256 of each oracle output.
+    with open(os.path.join(OUT, "c1_sha256.json"), "w") as f:
+        json.dump(c1_digests(), f, indent=1, sort_keys=True)
+        f.write("\n")
     print("golden fixtures written to", OUT)
+
+
+C1_SEED = SEED + 1
+
+
+def c1_digests():
+    """Config c1's inputs from C1_SEED (q, k, v ~ N(0,1) f16, norm weights
+    1 + N(0, 0.1)), the oracle's fused norm/RoPE/KV write and its f32 causal
+    attention on the written cache; SHA-256 of the output bytes (f16 bit
+    patterns, f32 little-endian)."""
+    g = np.random.default_rng(C1_SEED)
+    hq, hkv, S = 16, 8, 512
+    q, k, v = f16(g, (S, hq, D)), f16(g, (S, hkv, D)), f16(g, (S, hkv, D))
+    qw = (1 + 0.1 * g.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    kw = (1 + 0.1 * g.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    inv = oracle.build_inv_freq(THETA)
+    kc = np.zeros((hkv, S, D), np.float16)
+    vc = np.zeros((hkv, S, D), np.float16)
+    qo = oracle.qk_norm_rope_kv_prefill(q, k, v, qw, kw, inv, kc, vc, EPS, 0)
+    att = oracle.attn_prefill_f32(qo, kc, vc, 1.0 / math.sqrt(D), S, 0)
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()  # noqa: E731
+    return {"seed": C1_SEED, "shape": {"seq_len": S, "num_q_heads": hq, "num_kv_heads": hkv,
+                                       "head_dim": D, "max_seq_len": S},
+            "q_out_f16": sha(bits(qo)), "k_cache_f16": sha(bits(kc)),
+            "v_cache_f16": sha(bits(vc)), "attn_out_f32": sha(att.astype("<f4"))}
 
 
 if __name__ == "__main__":

@@ -205,6 +205,29 @@ def test_decode_fused_checks(L):
     assert call(12, -1.0) == -9                           # eps
 
 
+def test_decode_fused_noalloc_without_device(L):
+    """With no usable device the set-up fails with the HIP error, and the
+    failure is not kept: every later call tries again and reports its own
+    status (here the same error), never a stored one."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible: the set-up would succeed")
+    f = L.grout_attn_decode_fused_noalloc
+    args = [A] * 9 + [1e-6, 0x2DA8, 32, 8, 128, 4200, 32, 16, 1, None]
+    first = f(*args)
+    assert first > 0, first                       # a hipError_t, not a validation code
+    assert f(*args) == first
+    # Validation still runs before the device is touched.
+    bad = list(args)
+    bad[16] = 0                                   # num_splits
+    assert f(*bad) == -8
+    bad = list(args)
+    bad[12] = 256 * 3                             # num_kv_heads > 255, heads divisible
+    bad[11] = 256 * 3
+    assert f(*bad) == -11
+
+
 def test_kv_cache_update_checks(L):
     f = L.grout_kv_cache_update_seq
     # new_k, new_v, k_cache, v_cache, start, S, Hkv, D, MS, stream

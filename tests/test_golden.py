@@ -68,3 +68,20 @@ def test_attn_decode_fixture():
         assert np.array_equal(lse, z[f"nks{ns}_lse"])
         out = oracle.attn_decode_merge(att, lse, qg.shape[1])
         assert np.array_equal(out.view(np.uint16), z[f"nks{ns}_out"])
+
+
+def test_c1_output_digests():
+    """Config c1 end to end through the oracle (norm/RoPE/KV write, then f32
+    causal attention) reproduces the committed SHA-256 of every output."""
+    import json
+    import sys
+
+    sys.path.insert(0, GOLD)
+    try:
+        import make_golden
+    finally:
+        sys.path.remove(GOLD)
+    with open(os.path.join(GOLD, "c1_sha256.json")) as f:
+        want = json.load(f)
+    got = make_golden.c1_digests()
+    assert got == want

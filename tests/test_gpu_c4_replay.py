@@ -10,6 +10,7 @@ oracle under sustained replay.  Replays 0, 1, 500 and 999 are checked:
 attn_out against the oracle's norm/RoPE/KV write + split + merge at that
 position, q_out within 1 f16 ulp, every new K row within 1 ulp and every new V
 row bit-exact; at the end the position is 33768 and the counters are zero.
+Two further replays at one position must give bit-identical attn_out.
 """
 import numpy as np
 import pytest
@@ -89,5 +90,16 @@ def test_c4_graph_1000_replays_match_oracle(gpu):
         # Nothing past the last replay's slot was written.
         assert np.array_equal(dev["k_cache"][:, ctx + replays:].cpu().numpy().view(np.uint16),
                               kc[:, ctx + replays:].view(np.uint16))
+        # Two more replays at one position on identical inputs (each rewrites
+        # the same row): attn_out is bit-identical, the accumulation order
+        # being fixed.
+        outs = []
+        for _ in range(2):
+            runner.run(ctx + 500, 1)
+            runner.stream.synchronize()
+            outs.append(dev["attn_out"].clone())
+        print("[c4 replay] two replays at one position", flush=True)
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), \
+            "attn_out differs between two replays at one position"
     finally:
         runner.close()

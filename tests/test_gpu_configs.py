@@ -5,7 +5,9 @@
   an fp32 PyTorch attention computed on the GPU (itself checked against the
   oracle on the sampled rows).
 * c5 prefill, every row: the same fp32 PyTorch check at S=32768, 64/8 heads,
-  1% of K rows x8.
+  1% of K rows x8.  At both c3 and c5 the dynamic-schedule entry point
+  (grout_attn_prefill_sched, the bench's headline path) must give output
+  bit-identical to the static grid's and leave its counters at zero.
 * c5: Qwen3-32B causal prefill, S=32768, 64 Q / 8 KV heads, 1% of K rows x8
   (online-softmax rescale stress), then 64 decode steps appending to the same
   KV cache through the hipGraph runner (fused norm/RoPE/KV write + split-K +
@@ -114,7 +116,15 @@ def test_prefill_every_row_vs_torch_fp32(gpu, shape):
         dk[m] = (dk[m].float() * 8).half()
     out = torch.empty_like(dq)
     grout_amd.attend_prefill(dq, dk, dv, out, 0)
+    # The bench's headline entry point (the dynamic per-XCD schedule) on the
+    # same inputs: bit-identical to the static grid, counters left at zero.
+    counters = grout_amd.prefill_sched_counters()
+    out_sched = torch.full_like(dq, float("nan"))
+    grout_amd.attend_prefill(dq, dk, dv, out_sched, 0, sched_counters=counters)
     torch.cuda.synchronize()
+    assert torch.equal(out_sched.view(torch.int16), out.view(torch.int16)), "sched output differs"
+    assert int(counters.abs().sum().item()) == 0, "sched counters not left at zero"
+    del out_sched
     ref = _torch_causal_attention_f32(torch, dq, dk, dv, SCALE)
     # The GPU reference agrees with the oracle on a sample of rows, to fp32
     # summation-order differences (measured up to 1.1e-4 relative with the x8
