@@ -14,9 +14,9 @@
 //
 // Decode is HBM-bound (4-8 FLOP per byte); the kernel is shaped for bytes in
 // flight:
-//  * Workgroup = (split, kv_head), 4 wavefronts, one per CU (LDS-bound).
+//  * Workgroup = (split, kv_head), 4 wavefronts, one per CU.
 //    Each wavefront streams its own 16-token sub-chunks of the split (K 4 KB +
-//    V 4 KB each) through a private 4-stage LDS ring with direct HBM->LDS
+//    V 4 KB each) through a private 2-stage LDS ring with direct HBM->LDS
 //    copies; it waits only for its own copies, so the stream has no
 //    workgroup barrier, and the next copy goes out as soon as the operands
 //    of the current sub-chunk have been read.
@@ -54,9 +54,18 @@ constexpr int kDecThreads = kDecWaves * kWave;
 // of the split) through a private ring of kDecWaveStages stages; a stage is
 // the sub-chunk's K rows (4 KB) then its V rows (4 KB).  No workgroup barrier
 // is needed inside the stream.
+//
+// Two stages keep at most 64 KB of copies in flight per CU, 16 MB over the
+// chip, about what HBM's bandwidth times its loaded latency needs.  Measured
+// (fused step, caches cycled): 4 stages, twice that in flight, ran 3-11%
+// slower at every shape (Qwen3-32B 32K 26.8 vs 25.9 us, 8K 13.05 vs 11.65 us;
+// Qwen3-4B 4K 9.44 vs 8.95 us), 3 stages in between; 1 stage is too little
+// (26.97 us at 32K).  The surplus only queues in the memory system, where
+// some workgroups' requests wait longer than others' and the slowest
+// workgroup sets the end of the step.
 constexpr int kDecSubTok = 16;
 constexpr int kDecSubBytes = kDecSubTok * 256;
-constexpr int kDecWaveStages = 4;
+constexpr int kDecWaveStages = 2;
 constexpr int kDecWaveBytes = kDecWaveStages * 2 * kDecSubBytes;
 constexpr int kDecLdsBytes = kDecWaves * kDecWaveBytes;
 constexpr int kDecMinSplitTokens = 64;
@@ -328,7 +337,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
     const uint16_t* vh = a.v_cache + static_cast<int64_t>(kvh) * a.max_seq_len * kHeadDim;
 
     // Sub-chunk copy: sub-chunk `sub` of the split (tokens t0 + [0,16),
-    // t0 = tok_begin + 16*sub), this wavefront's k-th, lands in its stage k%4.  Copy i moves
+    // t0 = tok_begin + 16*sub), this wavefront's k-th, lands in its stage
+    // k % kDecWaveStages.  Copy i moves
     // token rows 4i..4i+3: 1 KB contiguous in the cache, 1 KB contiguous in
     // LDS.  Lane l takes row tr = 4i + l/16 and source chunk (l%16) ^ swz(tr),
     // so LDS chunk c of row tr holds global chunk c ^ swz(tr): the MFMA operand
@@ -466,7 +476,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
 
     for (int k = 0; k < nk; ++k) {
         // Sub-chunk k has landed once only the copies of this wavefront's later
-        // sub-chunks (8 each, up to three) are outstanding.
+        // sub-chunks (8 each, up to kDecWaveStages - 1 of them) are outstanding.
         const int younger = min(kDecWaveStages - 1, nk - 1 - k);
         if (younger >= 3) {
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(24));
@@ -492,8 +502,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         }
 
         // All LDS operands of the sub-chunk first: once they have arrived the
-        // stage takes sub-chunk k+4, so the copy goes out before the MFMA and
-        // softmax chain instead of after it.
+        // stage takes the wavefront's sub-chunk k + kDecWaveStages, so the copy
+        // goes out before the MFMA and softmax chain instead of after it.
         half8_t ka[4];
         half4_t va[8];
 #pragma unroll
@@ -636,17 +646,19 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         // 4(it%32)..+3 for it = t, t+256 (G <= 16); per 32 splits it reads
         // its LSEs as 16-byte vectors, then accumulates with independent
         // LDS reads, keeping an online (max, sum, acc) across chunks.
-        constexpr int kMergeRows = 448;
-        static_assert(kMergeRows * 256 + (kMergeRows + 31 * GROUT_MAX_DECODE_GROUP) * 4 <= kDecLdsBytes,
-                      "merge batch must fit the stages");
+        // 256 rows hold 32 splits of 8 query heads (Qwen3-32B) in one batch.
+        constexpr int kMergeRows = 256;
+        static_assert(kMergeRows * 256 <= kDecLdsBytes, "merge batch must fit the stages");
         static_assert(GROUT_MAX_DECODE_GROUP * 32 <= 2 * kDecThreads, "two merge items per thread");
+        // LSE table: G rows of SBp <= kMergeRows / G + 31 entries.
+        __shared__ float lse_tab[kMergeRows + 31 * GROUT_MAX_DECODE_GROUP];
         const int NS = a.num_splits;
         const int SB = kMergeRows / G;        // splits per batch
         const int SBp = (SB + 31) & ~31;      // row length of the LSE table
         const uint16_t* part_h = a.att_partial + static_cast<int64_t>(kvh) * NS * G * kHeadDim;
         const float* lse_h = a.lse_partial + static_cast<int64_t>(kvh) * NS * G;
         const unsigned char* rows_l = lds;
-        float* lse_t = reinterpret_cast<float*>(lds + kMergeRows * 256);
+        float* lse_t = lse_tab;
         // One batch of up to kMergeRows partial rows: rows into the stages,
         // LSEs into the [g][split] table (padded with -1e30 to SBp).
         auto load_batch = [&](int s0, int ns_b) {
