@@ -161,6 +161,30 @@ __device__ __forceinline__ void dec_lds_dma16_ptr_sc1(const void* gptr, uint32_t
 
 constexpr int dec_waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 16] (the count must be an
+// immediate, so each value has its own instruction).
+__device__ __forceinline__ void dec_wait_vm_upto16(int n) {
+    switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(1)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(2)); break;
+        case 3: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(3)); break;
+        case 4: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(4)); break;
+        case 5: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(5)); break;
+        case 6: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(6)); break;
+        case 7: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(7)); break;
+        case 8: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(8)); break;
+        case 9: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(9)); break;
+        case 10: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(10)); break;
+        case 11: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(11)); break;
+        case 12: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(12)); break;
+        case 13: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(13)); break;
+        case 14: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(14)); break;
+        case 15: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(15)); break;
+        default: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(16)); break;
+    }
+}
+
 // Per-workgroup inputs staged into LDS ahead of the K/V stream, 256 B rows:
 // split-only form: rows [0,G) = the G rotated query rows; fused form: rows
 // [0,G) = raw query rows of the QKV vector, then K row, V row, q_weight,
@@ -685,14 +709,47 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         if (NS <= SB && NS <= 64) {
             // All splits in one batch: the weights w_s = 2^(lse_s - M) of a
             // query row are computed once, by one 32-lane half per row (split
-            // s at lane s%32, s/32 its slot), and replace the LSEs in the table;
+            // s at lane s%32, s/32 its slot), into the [g][split] table;
             // then each thread sums its 4 dims over the splits.
-            load_batch(0, NS);
+            //
+            // When the head's NS*G LSEs fill whole 16-byte chunks at a
+            // 16-byte aligned address, wave 0 first copies them as stored
+            // ([split][g], sc1) into `pro`, free since the stream ended, and
+            // only then do the waves copy the partial rows.  Wave 0 waits for
+            // the LSE copies alone, so the weights are computed while the rows
+            // are still landing.
+            const int rows = NS * G;
+            const bool lse_first = (rows & 3) == 0 && (reinterpret_cast<uintptr_t>(lse_h) & 15) == 0;
+            static_assert(64 * GROUT_MAX_DECODE_GROUP * 4 <= kDecProDmas * 1024, "LSE block must fit `pro`");
+            const float* lse_raw = reinterpret_cast<const float*>(pro);
+            if (lse_first) {
+                if (wave == 0) {
+                    // Copy i moves LSEs 256i + [0, 256); lanes past the end
+                    // re-read the last chunk into slots past the table.
+                    for (int i = 0; i < (rows + 255) / 256; ++i)
+                        dec_lds_dma16_ptr_sc1(lse_h + min(256 * i + 4 * lane, rows - 4), pro0 + 1024u * i);
+                }
+                const int ncopies = rows / 4;
+                for (int i = wave; i < ncopies; i += kDecWaves)
+                    dec_lds_dma16_ptr_sc1(part_h + static_cast<int64_t>(4 * i + (lane >> 4)) * kHeadDim + 8 * (lane & 15),
+                                          lds0 + 1024u * i);
+                // Wave 0's row copies (at most 16) are younger than its LSE copies.
+                if (wave == 0) dec_wait_vm_upto16((ncopies + kDecWaves - 1) / kDecWaves);
+                lds_barrier();
+            } else {
+                load_batch(0, NS);
+            }
             for (int gi = tid >> 5; gi < G; gi += kDecThreads / 32) {
                 const int l = tid & 31;
                 float* lrow = lse_t + gi * SBp;
-                const float v0 = lrow[l];
-                const float v1 = NS > 32 ? lrow[32 + l] : kNegBig;
+                float v0, v1;
+                if (lse_first) {
+                    v0 = l < NS ? lse_raw[l * G + gi] : kNegBig;
+                    v1 = l + 32 < NS ? lse_raw[(l + 32) * G + gi] : kNegBig;
+                } else {
+                    v0 = lrow[l];
+                    v1 = NS > 32 ? lrow[32 + l] : kNegBig;
+                }
                 const float mx = half32_reduce(fmaxf(v0, v1), [](float x, float y) { return fmaxf(x, y); });
                 const float w0 = __builtin_amdgcn_exp2f(v0 - mx);
                 const float w1 = NS > 32 ? __builtin_amdgcn_exp2f(v1 - mx) : 0.0f;
@@ -701,6 +758,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
                 if (NS > 32) lrow[32 + l] = w1;
                 if (l == 0) s_wsum[gi] = sw;
             }
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
             lds_barrier();
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
