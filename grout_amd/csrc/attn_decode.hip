@@ -674,8 +674,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         constexpr int kMergeRows = 256;
         static_assert(kMergeRows * 256 <= kDecLdsBytes, "merge batch must fit the stages");
         static_assert(GROUT_MAX_DECODE_GROUP * 32 <= 2 * kDecThreads, "two merge items per thread");
-        // LSE table: G rows of SBp <= kMergeRows / G + 31 entries.
-        __shared__ float lse_tab[kMergeRows + 31 * GROUT_MAX_DECODE_GROUP];
+        // LSE table: G rows of SBp <= kMergeRows / G + 31 entries (16-byte
+        // aligned rows: the sums read them as float4).
+        __shared__ __attribute__((aligned(16))) float lse_tab[kMergeRows + 31 * GROUT_MAX_DECODE_GROUP];
         const int NS = a.num_splits;
         const int SB = kMergeRows / G;        // splits per batch
         const int SBp = (SB + 31) & ~31;      // row length of the LSE table
