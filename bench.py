@@ -952,7 +952,8 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(attention shards by KV head with no communication; see DESIGN.md).",
+              "(attention would shard by KV head with no communication, each GPU "
+              "running these kernels on its heads' share).",
               file=sys.stderr)
         return 2
     if not args.hip_default_graph_capture:
