@@ -338,6 +338,52 @@ def test_fused_consecutive_steps_advance(gpu):
     assert int(dpos.item()) == p0 + 10
 
 
+def test_fused_handoff_alternating_inputs(gpu):
+    """Stress of the merge hand-off at the c4 shape (64/8 heads, 32 splits, one
+    workgroup per CU): 400 launches at a fixed position alternate between two
+    QKV vectors, issued back to back on one stream.  The merger of each head
+    reads the partials its head's other workgroups published in the same
+    launch; a partial read before its store had landed would be the previous
+    launch's, computed from the other input, and would change the output.  So
+    every output equals the first output of its input bit for bit, the two
+    inputs' outputs differ, and the merge counters end at zero."""
+    import torch
+
+    import grout_amd
+    from tests._util import EPS, THETA
+
+    hq, hkv, pos, ns, n = 64, 8, 32768, 32, 400
+    MS, G = pos + 64, hq // hkv
+    gen = torch.Generator(device="cuda").manual_seed(4242)
+    dkc = torch.randn((hkv, MS, D), device="cuda", generator=gen).half()
+    dvc = torch.randn((hkv, MS, D), device="cuda", generator=gen).half()
+    qkvs = [torch.randn(((hq + 2 * hkv) * D,), device="cuda", generator=gen).half()
+            for _ in range(2)]
+    qw = (1.0 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    kw = (1.0 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    inv = torch.from_numpy(oracle.build_inv_freq(THETA)).cuda()
+    q_out = torch.zeros(((hq + hkv), D), dtype=torch.float16, device="cuda")
+    out = torch.zeros((hkv, G, D), dtype=torch.float16, device="cuda")
+    outs = torch.empty((n, hkv, G, D), dtype=torch.float16, device="cuda")
+    att, lse = grout_amd.decode_scratch(hkv, G, ns)
+    counters = grout_amd.decode_counters(hkv)
+    dpos = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    print(f"[handoff] {n} fused launches, {hq}/{hkv} heads, {ns} splits", flush=True)
+    for i in range(n):
+        grout_amd.decode_fused(qkvs[i % 2], qw, kw, inv, q_out, dkc, dvc, att, lse, out, counters,
+                               dpos, EPS, qk_scale_f16_bits(), hq, hkv)
+        outs[i].copy_(out)
+    torch.cuda.synchronize()
+    bits = outs.view(torch.int16)
+    for k in range(2):
+        same = (bits[k::2] == bits[k]).flatten(1).all(dim=1)
+        assert bool(same.all()), f"input {k}: launches {torch.nonzero(~same).flatten().tolist()[:8]} differ"
+    assert not torch.equal(bits[0], bits[1])
+    assert torch.isfinite(outs[:2].float()).all()
+    assert int(counters.view(torch.int32).abs().sum().item()) == 0
+    assert int(dpos.item()) == pos
+
+
 def test_fused_position_saturates_past_cache(gpu):
     """A fused step whose device position is at or past max_seq_len writes no
     cache row and, with advance_position, leaves the position where it is; the

@@ -84,6 +84,38 @@ def test_sched_two_calls_then_oracle_rows(gpu):
         assert_close_attn(on[r], o_ref, f"sched row {r}")
 
 
+def test_sched_alternating_inputs_reuse_output(gpu):
+    """Stress of the task queues at c3: 40 scheduled launches back to back on one
+    counter buffer and one output buffer, alternating between two query inputs.
+    A task claimed twice would only rewrite its block, but a task lost or a block
+    left unwritten would keep the previous launch's values, from the other input:
+    after every launch the whole output must equal the static grid's output for
+    that launch's input, bit for bit, and the counters must end at zero."""
+    import torch
+
+    import grout_amd
+
+    q_len, hq, hkv, n = 8192, 32, 8, 40
+    qa, kc, vc = _inputs(torch, 930, q_len, hq, hkv, q_len)
+    qb = _inputs(torch, 931, q_len, hq, hkv, q_len)[0]
+    refs = []
+    for q in (qa, qb):
+        r = torch.empty_like(q)
+        grout_amd.attend_prefill(q, kc, vc, r, 0)
+        refs.append(r.view(torch.int16))
+    counters = grout_amd.prefill_sched_counters()
+    out = torch.full_like(qa, float("nan"))
+    bad = torch.zeros((n,), dtype=torch.bool, device="cuda")
+    print(f"[prefill sched] {n} launches alternating two inputs", flush=True)
+    for i in range(n):
+        grout_amd.attend_prefill((qa, qb)[i % 2], kc, vc, out, 0, sched_counters=counters)
+        bad[i] = (out.view(torch.int16) != refs[i % 2]).any()
+    torch.cuda.synchronize()
+    assert not bool(bad.any()), f"launches {torch.nonzero(bad).flatten().tolist()[:8]} differ"
+    assert not torch.equal(refs[0], refs[1])
+    assert int(counters.abs().sum().item()) == 0
+
+
 def test_small_grid_takes_static_launch(gpu):
     """c1-sized grid (32 workgroups): static launch, counters untouched even
     when they hold a nonzero sentinel."""
