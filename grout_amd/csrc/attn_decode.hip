@@ -761,6 +761,51 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             }
             __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
             lds_barrier();
+            if (G * 64 <= kDecThreads) {
+                // G <= 4: thread t sums row g = t/64, dims 2(t%64)..+1, so all
+                // 256 threads share the rows (items of 4 dims would leave half
+                // of them idle).  Same per-element sums as below.
+                if (tid < G * 64) {
+                    const int g = tid >> 6, c = tid & 63;
+                    const float* wrow = lse_t + g * SBp;
+                    const unsigned char* rbase = rows_l + g * 256 + 4 * c;
+                    const int xstride = G * 256;
+                    float acc2[2] = {0.f, 0.f};
+                    for (int sc = 0; sc < NS; sc += 32) {
+                        if (NS - sc >= 32) {
+                            const unsigned char* xb = rbase + sc * xstride;
+                            half2_t xs[32];
+#pragma unroll
+                            for (int u = 0; u < 32; ++u)
+                                xs[u] = *reinterpret_cast<const half2_t*>(xb + u * xstride);
+                            float wv[32];
+#pragma unroll
+                            for (int u = 0; u < 8; ++u) {
+                                const float4_t w4 = *reinterpret_cast<const float4_t*>(wrow + sc + 4 * u);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) wv[4 * u + e] = w4[e];
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                            for (int u = 0; u < 32; ++u)
+#pragma unroll
+                                for (int e = 0; e < 2; ++e) acc2[e] += wv[u] * static_cast<float>(xs[u][e]);
+                        } else {
+                            for (int u = sc; u < NS; ++u) {
+                                const float w = wrow[u];
+                                const half2_t x = *reinterpret_cast<const half2_t*>(rbase + u * xstride);
+#pragma unroll
+                                for (int e = 0; e < 2; ++e) acc2[e] += w * static_cast<float>(x[e]);
+                            }
+                        }
+                    }
+                    const float inv = 1.0f / fmaxf(s_wsum[g], 1.0e-8f);
+                    half2_t h;
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) h[e] = static_cast<half_t>(acc2[e] * inv);
+                    *reinterpret_cast<half2_t*>(a.out + (static_cast<int64_t>(kvh) * G + g) * kHeadDim + 2 * c) = h;
+                }
+            } else {
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 const int it = tid + kDecThreads * k;
@@ -805,6 +850,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
                     *reinterpret_cast<half4_t*>(a.out + (static_cast<int64_t>(kvh) * G + g) * kHeadDim + 4 * c) = h;
                 }
             }
+            }  // G > 4
         } else {
         float m_i[2] = {-INFINITY, -INFINITY}, s_i[2] = {0.0f, 0.0f};
         float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};

@@ -23,8 +23,6 @@
 
 namespace grout {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
 // ------------------------------------------------------------------ norm --
 
 constexpr int kNormThreads = 1024;
