@@ -67,7 +67,13 @@ constexpr int kDecSubTok = 16;
 constexpr int kDecSubBytes = kDecSubTok * 256;
 constexpr int kDecWaveStages = 2;
 constexpr int kDecWaveBytes = kDecWaveStages * 2 * kDecSubBytes;
-constexpr int kDecLdsBytes = kDecWaves * kDecWaveBytes;
+// The stages (64 KB) and, after the stream, the fused merge's batch of
+// partial rows (128 KB) share one LDS buffer.  Its size does not limit the
+// stream: the grid is one workgroup per CU, and padding the kernel past half
+// of a CU's LDS measured the same.
+constexpr int kDecMergeLdsBytes = 128 * 1024;
+constexpr int kDecLdsBytes = kDecWaves * kDecWaveBytes > kDecMergeLdsBytes ? kDecWaves * kDecWaveBytes
+                                                                           : kDecMergeLdsBytes;
 constexpr int kDecMinSplitTokens = 64;
 // Chunk swizzle of a 256-byte token row in a stage: LDS chunk c of row tr
 // holds global chunk c ^ dec_swz(tr).  Distinct over the 16 rows (K reads:
@@ -161,27 +167,19 @@ __device__ __forceinline__ void dec_lds_dma16_ptr_sc1(const void* gptr, uint32_t
 
 constexpr int dec_waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
-// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 16] (the count must be an
-// immediate, so each value has its own instruction).
-__device__ __forceinline__ void dec_wait_vm_upto16(int n) {
-    switch (n) {
-        case 0: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0)); break;
-        case 1: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(1)); break;
-        case 2: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(2)); break;
-        case 3: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(3)); break;
-        case 4: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(4)); break;
-        case 5: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(5)); break;
-        case 6: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(6)); break;
-        case 7: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(7)); break;
-        case 8: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(8)); break;
-        case 9: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(9)); break;
-        case 10: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(10)); break;
-        case 11: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(11)); break;
-        case 12: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(12)); break;
-        case 13: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(13)); break;
-        case 14: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(14)); break;
-        case 15: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(15)); break;
-        default: __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(16)); break;
+// s_waitcnt vmcnt(min(n, N)) for a wave-uniform n >= 0: the count must be an
+// immediate, so each value has its own instruction (a chain of scalar
+// compares); a count above N waits for more than asked, never for less.
+template <int N>
+__device__ __forceinline__ void dec_wait_vm_atmost(int n) {
+    if constexpr (N == 0) {
+        __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(0));
+    } else {
+        if (n >= N) {
+            __builtin_amdgcn_s_waitcnt(dec_waitcnt_vm(N));
+        } else {
+            dec_wait_vm_atmost<N - 1>(n);
+        }
     }
 }
 
@@ -670,9 +668,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         // 4(it%32)..+3 for it = t, t+256 (G <= 16); per 32 splits it reads
         // its LSEs as 16-byte vectors, then accumulates with independent
         // LDS reads, keeping an online (max, sum, acc) across chunks.
-        // 256 rows hold 32 splits of 8 query heads (Qwen3-32B) in one batch.
-        constexpr int kMergeRows = 256;
-        static_assert(kMergeRows * 256 <= kDecLdsBytes, "merge batch must fit the stages");
+        // 512 rows hold the 32 splits of 16 query heads, or the 64 splits of
+        // 8 that grout_attn_decode_pick_splits gives 4 KV heads, in one batch.
+        constexpr int kMergeRows = 512;
+        static_assert(kMergeRows * 256 <= kDecLdsBytes, "merge batch must fit the LDS buffer");
         static_assert(GROUT_MAX_DECODE_GROUP * 32 <= 2 * kDecThreads, "two merge items per thread");
         // LSE table: G rows of SBp <= kMergeRows / G + 31 entries (16-byte
         // aligned rows: the sums read them as float4).
@@ -721,7 +720,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
             // are still landing.
             const int rows = NS * G;
             const bool lse_first = (rows & 3) == 0 && (reinterpret_cast<uintptr_t>(lse_h) & 15) == 0;
-            static_assert(64 * GROUT_MAX_DECODE_GROUP * 4 <= kDecProDmas * 1024, "LSE block must fit `pro`");
+            static_assert(kMergeRows * 4 <= kDecProDmas * 1024, "LSE block (rows <= kMergeRows) must fit `pro`");
             const float* lse_raw = reinterpret_cast<const float*>(pro);
             if (lse_first) {
                 if (wave == 0) {
@@ -734,8 +733,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
                 for (int i = wave; i < ncopies; i += kDecWaves)
                     dec_lds_dma16_ptr_sc1(part_h + static_cast<int64_t>(4 * i + (lane >> 4)) * kHeadDim + 8 * (lane & 15),
                                           lds0 + 1024u * i);
-                // Wave 0's row copies (at most 16) are younger than its LSE copies.
-                if (wave == 0) dec_wait_vm_upto16((ncopies + kDecWaves - 1) / kDecWaves);
+                // Wave 0's row copies (at most kMergeRows / 16 = 32) are younger
+                // than its LSE copies.
+                static_assert(kMergeRows / 16 <= 32, "row copies per wave within the wait");
+                if (wave == 0) dec_wait_vm_atmost<32>((ncopies + kDecWaves - 1) / kDecWaves);
                 lds_barrier();
             } else {
                 load_batch(0, NS);

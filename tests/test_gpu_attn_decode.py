@@ -219,14 +219,16 @@ def _fused_case(seed, hq, hkv, MS):
     (4, 2, 0, 8, 4, 73),           # s_kv = 1, empty splits
     (16, 16, 300, 512, 3, 74),     # G = 1; 3 LSEs: not whole 16-byte chunks, so the
                                    # merge loads them with the rows (fallback path)
-    # The in-kernel merge takes its partial rows in batches of 256 / G splits
-    # and carries (max, sum, acc) across them; these need 2-4 batches.
-    (32, 4, 4100, 4200, 64, 76),   # G = 8: batches of 32 splits (32 + 32)
-    (64, 4, 3000, 3100, 40, 77),   # G = 16: batches of 16 (16 + 16 + 8)
-    (48, 4, 4000, 4100, 75, 78),   # G = 12: batches of 21 (21 + 21 + 21 + 12)
-    (64, 4, 5000, 5100, 64, 79),   # G = 16: 16 + 16 + 16 + 16
-    (64, 8, 3000, 3100, 48, 80),   # G = 8: 32 + 16
+    # The in-kernel merge takes its partial rows in batches of 512 / G splits
+    # (one batch at most 64 splits) and carries (max, sum, acc) across them;
+    # these need 2-3 batches.
+    (32, 4, 4100, 4200, 96, 76),   # G = 8: batches of 64 splits (64 + 32)
+    (64, 4, 3000, 3100, 40, 77),   # G = 16: batches of 32 (32 + 8)
+    (48, 4, 4000, 4100, 100, 78),  # G = 12: batches of 42 (42 + 42 + 16)
+    (64, 4, 5000, 5100, 64, 79),   # G = 16: 32 + 32 (4 KV heads' picked split count)
     # One batch, LSE block copied first.
+    (64, 8, 3000, 3100, 48, 80),   # G = 8, 48 splits: two weight slots per lane
+    (32, 4, 4100, 4200, 64, 84),   # G = 8, 64 splits (4 KV heads' picked split count)
     (64, 4, 2500, 2600, 16, 81),   # G = 16, 16 splits: two passes of the weight rows
     (32, 8, 3000, 3100, 48, 82),   # G = 4, 48 splits: two weight slots per lane
     # One batch, fallback path (105 LSEs), two weight slots per lane.

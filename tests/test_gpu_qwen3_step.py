@@ -270,23 +270,23 @@ def test_runner_step_after_eager_step_writes_position(gpu):
 
 
 def test_runner_picked_splits_two_kv_heads_multi_batch_merge(gpu):
-    """A runner at Hkv=4, G=8 with grout_attn_decode_pick_splits' count (64 on
+    """A runner at Hkv=4, G=16 with grout_attn_decode_pick_splits' count (64 on
     256 CUs): the fused merge folds its 64 splits in two batches of partial
-    rows, carrying the online max/sum across them."""
+    rows (32 splits of 16 rows each), carrying the online max/sum across them."""
     import torch
     import grout_amd
 
-    m = qwen3_tiny_model(1750, layers=1, hidden=256, hq=32, hkv=4, inter=256, vocab=512,
+    m = qwen3_tiny_model(1750, layers=1, hidden=256, hq=64, hkv=4, inter=256, vocab=512,
                          max_seq=4200, filled=4100)
     ref = copy.deepcopy(m)
     dm = _device_model(torch, m)
     ns = grout_amd.pick_num_splits(4200, 4)
-    print(f"[qwen3 step] Hkv=4 G=8 picked splits {ns}", flush=True)
+    print(f"[qwen3 step] Hkv=4 G=16 picked splits {ns}", flush=True)
     token = torch.tensor([3], dtype=torch.int32, device="cuda")
     position = torch.zeros((1,), dtype=torch.int32, device="cuda")
     logits = torch.zeros((512,), dtype=torch.float16, device="cuda")
     runner = grout_amd.Qwen3DecodeRunner(
-        **dm, token=token, position=position, logits=logits, num_q_heads=32, num_kv_heads=4,
+        **dm, token=token, position=position, logits=logits, num_q_heads=64, num_kv_heads=4,
         eps=m["eps"], qk_scale_f16_bits=m["qk_scale_f16_bits"], num_splits=ns, block_n=32,
         prime_position=4100)
     try:
