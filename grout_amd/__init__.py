@@ -425,7 +425,7 @@ class Qwen3DecodeRunner:
             _ensure(t.dtype in (torch.int32, torch.uint32) and t.is_cuda and t.numel() >= 1,
                     f"{nm} must be a device int32 tensor")
         if num_splits is None:
-            num_splits = pick_num_splits(max_seq, hkv, block_n)
+            num_splits = pick_num_splits(max_seq, hkv, block_n, group=hq // hkv)
         self._layers = (_lib.Qwen3Layer * len(layers))(*[
             _lib.Qwen3Layer(**{key: _ptr(L[key]) for key in QWEN3_LAYER_KEYS}) for L in layers])
         M = _lib.Qwen3Model(
@@ -487,13 +487,15 @@ class Qwen3DecodeRunner:
 
 
 def pick_num_splits(max_context: int, num_kv_heads: int, block_n: int = ATTN_BN_DECODE,
-                    device: int | None = None) -> int:
+                    device: int | None = None, group: int = 1) -> int:
+    """Split count of the decode graph for this device's CU count
+    (grout_attn_decode_pick_splits_grouped; group = query heads per KV head)."""
     torch = _torch()
     cu = ctypes.c_int32(0)
     dev = torch.cuda.current_device() if device is None else device
     _check(lib().grout_device_cu_count(dev, ctypes.byref(cu)), "device_cu_count")
-    return int(lib().grout_attn_decode_pick_splits(cu.value, num_kv_heads, max_context,
-                                                   block_n))
+    return int(lib().grout_attn_decode_pick_splits_grouped(cu.value, num_kv_heads, group,
+                                                           max_context, block_n))
 
 
 def decode_scratch(num_kv_heads: int, group: int, num_splits: int, head_dim: int = HEAD_DIM,

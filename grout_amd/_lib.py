@@ -111,6 +111,7 @@ SIGNATURES = {
     "grout_attn_decode_partial_bytes": (c_i64, [c_i32] * 4),
     "grout_attn_decode_lse_bytes": (c_i64, [c_i32] * 3),
     "grout_attn_decode_pick_splits": (c_i32, [c_i32] * 4),
+    "grout_attn_decode_pick_splits_grouped": (c_i32, [c_i32] * 5),
     "grout_device_cu_count": (c_i32, [c_i32, ctypes.POINTER(c_i32)]),
     "grout_graph_begin": (c_i32, [c_vp]),
     "grout_graph_end": (c_i32, [c_vp, ctypes.POINTER(c_vp)]),

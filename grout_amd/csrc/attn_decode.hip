@@ -72,6 +72,9 @@ constexpr int kDecWaveBytes = kDecWaveStages * 2 * kDecSubBytes;
 // stream: the grid is one workgroup per CU, and padding the kernel past half
 // of a CU's LDS measured the same.
 constexpr int kDecMergeLdsBytes = 128 * 1024;
+// Partial rows (256 B each) of one merge batch: the 32 splits of 16 query
+// heads, or the 64 splits of 8 that 4 KV heads take on 256 CUs.
+constexpr int kDecMergeRows = kDecMergeLdsBytes / 256;
 constexpr int kDecLdsBytes = kDecWaves * kDecWaveBytes > kDecMergeLdsBytes ? kDecWaves * kDecWaveBytes
                                                                            : kDecMergeLdsBytes;
 constexpr int kDecMinSplitTokens = 64;
@@ -668,9 +671,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         // 4(it%32)..+3 for it = t, t+256 (G <= 16); per 32 splits it reads
         // its LSEs as 16-byte vectors, then accumulates with independent
         // LDS reads, keeping an online (max, sum, acc) across chunks.
-        // 512 rows hold the 32 splits of 16 query heads, or the 64 splits of
-        // 8 that grout_attn_decode_pick_splits gives 4 KV heads, in one batch.
-        constexpr int kMergeRows = 512;
+        constexpr int kMergeRows = kDecMergeRows;
         static_assert(kMergeRows * 256 <= kDecLdsBytes, "merge batch must fit the LDS buffer");
         static_assert(GROUT_MAX_DECODE_GROUP * 32 <= 2 * kDecThreads, "two merge items per thread");
         // LSE table: G rows of SBp <= kMergeRows / G + 31 entries (16-byte
@@ -1230,19 +1231,32 @@ extern "C" int64_t grout_attn_decode_counter_bytes(int32_t num_kv_heads) {
     return static_cast<int64_t>(num_kv_heads + 1) * kDecCounterStride * 4;
 }
 
-extern "C" int32_t grout_attn_decode_pick_splits(int32_t cu_count, int32_t num_kv_heads,
-                                                 int32_t max_context, int32_t block_n) {
+extern "C" int32_t grout_attn_decode_pick_splits_grouped(int32_t cu_count, int32_t num_kv_heads,
+                                                         int32_t group, int32_t max_context,
+                                                         int32_t block_n) {
     if (cu_count <= 0) cu_count = 256;
     if (num_kv_heads <= 0 || block_n <= 0 || max_context <= 0) return 1;
-    // One workgroup per CU (each holds ~130 KB of LDS stages) streaming at the
-    // longest context; a split shorter than kDecMinSplitTokens spends more on
-    // its prologue and the merge than it saves.
+    if (group <= 0) group = 1;
+    // One workgroup per CU streaming at the longest context; a split shorter
+    // than kDecMinSplitTokens spends more on its prologue and the merge than
+    // it saves.
     const int64_t tiles = (static_cast<int64_t>(max_context) + block_n - 1) / block_n;
     const int64_t min_tiles = (kDecMinSplitTokens + block_n - 1) / block_n;
     int64_t want = (static_cast<int64_t>(cu_count) + num_kv_heads - 1) / num_kv_heads;
+    // The fused merge loads NS * G partial rows through one CU per KV head:
+    // keep them to one batch where that still keeps half the CUs streaming
+    // (64 Q / 4 KV heads at 32K: 64 splits 21.9 us, 32 splits 20.3 us).
+    const int64_t one_batch = kDecMergeRows / group;
+    const int64_t half_cus = (static_cast<int64_t>(cu_count) / 2 + num_kv_heads - 1) / num_kv_heads;
+    if (want > one_batch) want = one_batch > half_cus ? one_batch : half_cus;
     const int64_t cap = (tiles + min_tiles - 1) / min_tiles;
     if (want > cap) want = cap;
     if (want < 1) want = 1;
     if (want > GROUT_MAX_DECODE_SPLITS) want = GROUT_MAX_DECODE_SPLITS;
     return static_cast<int32_t>(want);
+}
+
+extern "C" int32_t grout_attn_decode_pick_splits(int32_t cu_count, int32_t num_kv_heads,
+                                                 int32_t max_context, int32_t block_n) {
+    return grout_attn_decode_pick_splits_grouped(cu_count, num_kv_heads, 1, max_context, block_n);
 }

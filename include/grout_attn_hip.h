@@ -359,6 +359,15 @@ int64_t grout_attn_decode_lse_bytes(int32_t num_kv_heads, int32_t group, int32_t
 int32_t grout_attn_decode_pick_splits(int32_t cu_count, int32_t num_kv_heads,
                                       int32_t max_context, int32_t block_n);
 
+/* The same count given the query heads per KV head (group): where the splits
+ * of a KV head times group exceed the 512 partial rows grout_attn_decode_fused
+ * merges in one batch, it takes fewer splits, as long as at least half the
+ * CUs keep streaming (64 Q / 4 KV heads on 256 CUs: 32 splits rather than
+ * 64).  group = 1 gives grout_attn_decode_pick_splits.  Returns >= 1. */
+int32_t grout_attn_decode_pick_splits_grouped(int32_t cu_count, int32_t num_kv_heads,
+                                              int32_t group, int32_t max_context,
+                                              int32_t block_n);
+
 /* Number of compute units of a device (hipDeviceAttributeMultiprocessorCount). */
 int32_t grout_device_cu_count(int32_t device, int32_t* cu_count);
 

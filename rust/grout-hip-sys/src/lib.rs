@@ -259,6 +259,9 @@ extern "C" {
     pub fn grout_attn_decode_pick_splits(
         cu_count: i32, num_kv_heads: i32, max_context: i32, block_n: i32,
     ) -> i32;
+    pub fn grout_attn_decode_pick_splits_grouped(
+        cu_count: i32, num_kv_heads: i32, group: i32, max_context: i32, block_n: i32,
+    ) -> i32;
     pub fn grout_device_cu_count(device: i32, cu_count: *mut i32) -> i32;
 
     pub fn grout_graph_begin(stream: HipStream) -> i32;

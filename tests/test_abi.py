@@ -388,6 +388,25 @@ def test_pick_splits(L):
         assert 1 <= f(256, 8, ctx, 32) <= 1024
 
 
+def test_pick_splits_grouped(L):
+    f, g = L.grout_attn_decode_pick_splits, L.grout_attn_decode_pick_splits_grouped
+    # group 1 is the ungrouped count, at every context and head count.
+    for hkv in (1, 2, 4, 8, 16):
+        for ctx in (1, 100, 4097, 33792, 10 ** 6):
+            assert g(256, hkv, 1, ctx, 32) == f(256, hkv, ctx, 32)
+    # NS * G within one 512-row merge batch leaves the count alone.
+    assert g(256, 8, 8, 32768, 32) == 32         # Qwen3-32B
+    assert g(256, 8, 4, 32768, 32) == 32         # Qwen3-4B
+    assert g(256, 4, 8, 32768, 32) == 64         # 32 Q / 4 KV heads: 64 x 8 = 512
+    # Beyond one batch it takes the batch's split count while that keeps half the CUs.
+    assert g(256, 4, 16, 32768, 32) == 32        # 64 Q / 4 KV heads
+    assert g(256, 4, 12, 32768, 32) == 42        # 512 // 12
+    assert g(256, 2, 16, 32768, 32) == 64        # half the CUs: 128 / 2 KV heads
+    # Short contexts still get no split shorter than one 64-token chunk.
+    assert g(256, 4, 16, 1000, 32) == (1000 + 63) // 64
+    assert g(256, 4, 0, 32768, 32) == f(256, 4, 32768, 32)   # group <= 0 reads as 1
+
+
 def test_python_mirror_shape_errors():
     torch = pytest.importorskip("torch")
     import grout_amd
