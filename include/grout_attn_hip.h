@@ -301,7 +301,8 @@ int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_pa
  * only validated) and the LSE merge into out
  * [num_kv_heads, group, 128].  The last workgroup of each KV head merges: it
  * is found by an agent-scope counter in `counters`, and the partials reach it
- * through device-coherent stores completed before that counter moves.
+ * through device-coherent stores completed before that counter moves.  Every
+ * sum runs in a fixed order, so identical inputs give a bit-identical out.
  *   counters: grout_attn_decode_counter_bytes(num_kv_heads) bytes, zero
  *   before the first call; every call leaves them zero again.
  *   advance_position != 0: the launch ends by storing *d_position + 1, so a
