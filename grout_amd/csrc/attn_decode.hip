@@ -67,16 +67,19 @@ constexpr int kDecSubTok = 16;
 constexpr int kDecSubBytes = kDecSubTok * 256;
 constexpr int kDecWaveStages = 2;
 constexpr int kDecWaveBytes = kDecWaveStages * 2 * kDecSubBytes;
-// The stages (64 KB) and, after the stream, the fused merge's batch of
-// partial rows (128 KB) share one LDS buffer.  Its size does not limit the
-// stream: the grid is one workgroup per CU, and padding the kernel past half
-// of a CU's LDS measured the same.
+// The stages (64 KB) and, after the stream, the wave combine and (fused form)
+// the merge's batch of partial rows (128 KB) share one LDS buffer.  The
+// larger fused buffer does not limit the stream: the fused grid is one
+// workgroup per CU, and padding the kernel past half of a CU's LDS measured
+// the same.  The split-only form keeps the stage size, so two of its
+// workgroups still share a CU when its grid is larger than the CU count.
+constexpr int kDecStageLdsBytes = kDecWaves * kDecWaveBytes;
 constexpr int kDecMergeLdsBytes = 128 * 1024;
 // Partial rows (256 B each) of one merge batch: the 32 splits of 16 query
 // heads, or the 64 splits of 8 that 4 KV heads take on 256 CUs.
 constexpr int kDecMergeRows = kDecMergeLdsBytes / 256;
-constexpr int kDecLdsBytes = kDecWaves * kDecWaveBytes > kDecMergeLdsBytes ? kDecWaves * kDecWaveBytes
-                                                                           : kDecMergeLdsBytes;
+constexpr int kDecFusedLdsBytes = kDecStageLdsBytes > kDecMergeLdsBytes ? kDecStageLdsBytes
+                                                                        : kDecMergeLdsBytes;
 constexpr int kDecMinSplitTokens = 64;
 // Chunk swizzle of a 256-byte token row in a stage: LDS chunk c of row tr
 // holds global chunk c ^ dec_swz(tr).  Distinct over the 16 rows (K reads:
@@ -95,7 +98,7 @@ constexpr float kDecRescaleSlack = 8.0f;
 // serialise on one line.
 constexpr int kDecCounterStride = 64;  // u32 elements
 
-static_assert(kDecWaves * kDecRedStride * 4 <= kDecLdsBytes,
+static_assert(kDecWaves * kDecRedStride * 4 <= kDecStageLdsBytes,
               "wave combine reuses the stage buffers");
 
 struct DecodeArgs {
@@ -274,7 +277,7 @@ __device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t 
 
 template <bool kFused>
 __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs a) {
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[kDecLdsBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kFused ? kDecFusedLdsBytes : kDecStageLdsBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char pro[kDecProDmas * 1024];
     __shared__ __attribute__((aligned(16))) half_t q_lds[GROUT_MAX_DECODE_GROUP * kHeadDim];
     __shared__ float s_cos[64], s_sin[64];
@@ -672,7 +675,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void attn_decode_kernel(DecodeArgs 
         // its LSEs as 16-byte vectors, then accumulates with independent
         // LDS reads, keeping an online (max, sum, acc) across chunks.
         constexpr int kMergeRows = kDecMergeRows;
-        static_assert(kMergeRows * 256 <= kDecLdsBytes, "merge batch must fit the LDS buffer");
+        static_assert(kMergeRows * 256 <= kDecFusedLdsBytes, "merge batch must fit the LDS buffer");
         static_assert(GROUT_MAX_DECODE_GROUP * 32 <= 2 * kDecThreads, "two merge items per thread");
         // LSE table: G rows of SBp <= kMergeRows / G + 31 entries (16-byte
         // aligned rows: the sums read them as float4).
