@@ -303,6 +303,9 @@ int32_t grout_attn_decode_merge(const uint16_t* att_partial, const float* lse_pa
  * is found by an agent-scope counter in `counters`, and the partials reach it
  * through device-coherent stores completed before that counter moves.  Every
  * sum runs in a fixed order, so identical inputs give a bit-identical out.
+ * A workgroup takes 143 KB of LDS (the merge's batch buffer), one per CU:
+ * num_splits * num_kv_heads beyond the CU count runs in rounds, so take the
+ * count from grout_attn_decode_pick_splits_grouped.
  *   counters: grout_attn_decode_counter_bytes(num_kv_heads) bytes, zero
  *   before the first call; every call leaves them zero again.
  *   advance_position != 0: the launch ends by storing *d_position + 1, so a
