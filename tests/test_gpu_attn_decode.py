@@ -229,6 +229,7 @@ def _fused_case(seed, hq, hkv, MS):
     # One batch, LSE block copied first.
     (64, 8, 3000, 3100, 48, 80),   # G = 8, 48 splits: two weight slots per lane
     (32, 4, 4100, 4200, 64, 84),   # G = 8, 64 splits (4 KV heads' picked split count)
+    (64, 4, 5000, 5100, 32, 85),   # G = 16, 32 splits: 512 rows, the grouped picker's count
     (64, 4, 2500, 2600, 16, 81),   # G = 16, 16 splits: two passes of the weight rows
     (32, 8, 3000, 3100, 48, 82),   # G = 4, 48 splits: two weight slots per lane
     # One batch, fallback path (105 LSEs), two weight slots per lane.
