@@ -417,3 +417,62 @@ def test_fused_position_saturates_past_cache(gpu):
         assert int(counters.abs().sum().item()) == 0
         if start >= MS:
             assert torch.equal(before_k, dkc), "a position past the cache wrote a K row"
+
+
+def test_fused_steps_on_two_streams_concurrently(gpu):
+    """Two streams, each with its own scratch, counters, position and output,
+    run 50 fused decode steps each, interleaved on the host so their launches
+    overlap on the GPU (c4 heads, 32 splits: 256 workgroups each, so the two
+    grids share the CUs).  Each stream's outputs equal the same steps run
+    alone, bit for bit: the kernel keeps no state outside its arguments."""
+    import torch
+
+    import grout_amd
+    from tests._util import EPS, THETA
+
+    hq, hkv, pos, ns, n = 64, 8, 8192, 32, 50
+    MS, G = pos + 64, hq // hkv
+    gen = torch.Generator(device="cuda").manual_seed(5151)
+    inv = torch.from_numpy(oracle.build_inv_freq(THETA)).cuda()
+    qw = (1.0 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+    kw = (1.0 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
+
+    def state():
+        kc = torch.randn((hkv, MS, D), device="cuda", generator=gen).half()
+        vc = torch.randn((hkv, MS, D), device="cuda", generator=gen).half()
+        qkv = torch.randn(((hq + 2 * hkv) * D,), device="cuda", generator=gen).half()
+        att, lse = grout_amd.decode_scratch(hkv, G, ns)
+        return dict(kc=kc, vc=vc, qkv=qkv, att=att, lse=lse,
+                    counters=grout_amd.decode_counters(hkv),
+                    q_out=torch.zeros(((hq + hkv), D), dtype=torch.float16, device="cuda"),
+                    out=torch.zeros((hkv, G, D), dtype=torch.float16, device="cuda"),
+                    outs=torch.empty((n, hkv, G, D), dtype=torch.float16, device="cuda"))
+
+    def launch(s, i):
+        grout_amd.decode_fused(s["qkv"], qw, kw, inv, s["q_out"], s["kc"], s["vc"], s["att"],
+                               s["lse"], s["out"], s["counters"], s["pos"], EPS,
+                               qk_scale_f16_bits(), hq, hkv, advance_position=True)
+        s["outs"][i].copy_(s["out"])
+
+    sts = [state(), state()]
+    snap = [{k: v.clone() for k, v in s.items()} for s in sts]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    print(f"[two streams] {n} fused steps each, interleaved", flush=True)
+    for s in sts:
+        s["pos"] = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    for i in range(n):
+        for s, st in zip(sts, streams):
+            with torch.cuda.stream(st):
+                launch(s, i)
+    torch.cuda.synchronize()
+    # The same steps, one stream at a time, from the saved starting state.
+    for s, ref in zip(sts, snap):
+        ref["pos"] = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        for i in range(n):
+            launch(ref, i)
+        torch.cuda.synchronize()
+        assert torch.equal(s["outs"].view(torch.int16), ref["outs"].view(torch.int16))
+        assert torch.equal(s["kc"].view(torch.int16), ref["kc"].view(torch.int16))
+        assert int(s["pos"].item()) == pos + n
+        assert int(s["counters"].abs().sum().item()) == 0
