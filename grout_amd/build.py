@@ -43,13 +43,22 @@ HIP_FLAGS = [
 ]
 
 
+#: Flags for single files.  The decode kernels take the device position
+#: pointer as their first argument; preloading the first two arguments into
+#: SGPRs (gfx940+ kernel-argument preload) lets the position load go out at
+#: the kernel's first instruction.
+FILE_FLAGS = {
+    "attn_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=2"],
+}
+
+
 def sources(d: str = CSRC) -> list[str]:
     return sorted(os.path.join(d, f) for f in os.listdir(d) if f.endswith(".hip"))
 
 
 def _compile(src: str, verbose: bool, extra: list[str]) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, *extra, "-c", src, "-o", obj]
+    cmd = [HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), *extra, "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
