@@ -149,6 +149,33 @@ def time_back_to_back(torch, fn, n: int, warmup: int, stream=None) -> float:
     return a.elapsed_time(b) / n
 
 
+def time_graph_cycle(torch, fn, per_graph: int, launches: int, stream) -> float:
+    """Average duration (ms) of one launch of fn, from events around replays of a
+    hipGraph that holds `per_graph` consecutive calls of fn (about `launches`
+    launches in all): launches back to back on the device without the host's
+    per-launch cost, which is longer than a short kernel such as c2's decode
+    step (issued from Python, c2's step measured ~1.5 us longer than its kernel
+    trace).  fn must not synchronize (it is captured)."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(per_graph):
+            fn()
+    replays = max(3, -(-launches // per_graph))
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            g.replay()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(replays):
+            g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+    del g
+    return a.elapsed_time(b) / (replays * per_graph)
+
+
 def bench_prefill(torch, ga, steps, warmup, gen):
     hq, hkv, S = 32, 8, 8192
     q = torch.randn((S, hq, D), device="cuda", generator=gen, dtype=torch.float32).half()
@@ -392,18 +419,18 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps, gra
         return dict(step_us=step_us, step_gbs=avg_bytes / (step_us * 1e-6) / 1e9,
                     replays=replays)
 
-    # The fused step alone (the graph's only kernel), eager at position ctx
-    # (s_kv = ctx + 1, position not advanced), back-to-back launches; then the
-    # standalone split and merge ops of the same shape.
+    # The fused step alone (the graph's only kernel) at position ctx (s_kv =
+    # ctx + 1, position not advanced), launched back to back from a captured
+    # graph; then the standalone split and merge ops of the same shape.
     counters = ga.decode_counters(hkv)
     pos_t.fill_(ctx)
     with torch.cuda.stream(s):
         ffn = lambda: ga.decode_fused(qkv, qw, kw, inv, q_out, kc, vc, att, lse, attn_out,  # noqa
                                       counters, pos_t, EPS, scale_bits, hq, hkv)
-        fused_us = 1e3 * time_back_to_back(torch, ffn, split_steps, 10, stream=s)
+        fused_us = 1e3 * time_graph_cycle(torch, ffn, 16, split_steps, s)
         q_grouped = q_out[:hq].view(hkv, G, D)
         fn = lambda: ga.fmha_decode_gqa_split(q_grouped, kc, vc, att, lse, scale_bits, pos_t)  # noqa
-        split_us = 1e3 * time_back_to_back(torch, fn, split_steps, 10, stream=s)
+        split_us = 1e3 * time_graph_cycle(torch, fn, 16, split_steps, s)
         # The same fused step cycling through several layers' caches, so no
         # launch finds its K/V in the 256 MB last-level cache: the situation of
         # a real token step, where the other layers run between two reads of
@@ -418,13 +445,13 @@ def bench_decode(torch, ga, hq, hkv, ctx, replays, warmup, gen, split_steps, gra
             c = it[0] % nc
             ga.decode_fused(qkv, qw, kw, inv, q_out, kcs[c], vcs[c], att, lse, attn_out,
                             counters, pos_t, EPS, scale_bits, hq, hkv)
-        cold_us = 1e3 * time_back_to_back(torch, cold, split_steps, 3 * nc, stream=s)
+        cold_us = 1e3 * time_graph_cycle(torch, cold, 4 * nc, split_steps, s)
 
         def split_cold():
             it[0] += 1
             c = it[0] % nc
             ga.fmha_decode_gqa_split(q_grouped, kcs[c], vcs[c], att, lse, scale_bits, pos_t)
-        split_cold_us = 1e3 * time_back_to_back(torch, split_cold, split_steps, 3 * nc, stream=s)
+        split_cold_us = 1e3 * time_graph_cycle(torch, split_cold, 4 * nc, split_steps, s)
         del kcs, vcs
         mfn = lambda: ga.splitk_reduce_merge(att, lse, attn_out)  # noqa: E731
         # A ~4 us kernel launched back to back through the Python mirror is
@@ -483,16 +510,20 @@ def bench_decode_layer(torch, ga, steps, gen):
     w = (1 + 0.1 * torch.randn((n,), device="cuda", generator=gen)).half()
     o = torch.empty_like(r)
     ro = torch.empty_like(r)
-    args = (r.data_ptr(), x.data_ptr(), w.data_ptr(), o.data_ptr(), ro.data_ptr(), EPS, n, st)
-    res["add_rms_norm"] = dict(n=n, us=1e3 * time_back_to_back(
-        torch, lambda: L.grout_add_rms_norm_decode(*args), max(steps, 200), 20))
+    # The two short kernels run back to back from a captured graph (the stream
+    # is looked up at each call: the capture stream).
+    cur = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    args = (r.data_ptr(), x.data_ptr(), w.data_ptr(), o.data_ptr(), ro.data_ptr(), EPS, n)
+    gs = torch.cuda.Stream()
+    res["add_rms_norm"] = dict(n=n, us=1e3 * time_graph_cycle(
+        torch, lambda: L.grout_add_rms_norm_decode(*args, cur()), 50, max(steps, 200), gs))
     v = 151936
     lg = torch.randn((v,), device="cuda", generator=gen).half()
     bm, bi = ga.argmax_scratch(v)
     tok = torch.empty((1,), device="cuda", dtype=torch.int32)
-    aargs = (lg.data_ptr(), bm.data_ptr(), bi.data_ptr(), tok.data_ptr(), v, st)
-    res["argmax"] = dict(n=v, us=1e3 * time_back_to_back(
-        torch, lambda: L.grout_argmax_f16(*aargs), max(steps, 200), 20))
+    aargs = (lg.data_ptr(), bm.data_ptr(), bi.data_ptr(), tok.data_ptr(), v)
+    res["argmax"] = dict(n=v, us=1e3 * time_graph_cycle(
+        torch, lambda: L.grout_argmax_f16(*aargs, cur()), 50, max(steps, 200), gs))
     assert int(tok.item()) == int(torch.argmax(lg.float()).item()), "argmax mismatch"
     return res
 
@@ -639,7 +670,8 @@ def bench_hbm_probe(torch, gib: int = 4, launches: int = 5):
 def bench_prefill_c1(torch, ga, gen, n: int = 200):
     """c1: Qwen3-0.6B layer, S=512, 16 Q / 8 KV heads: the fused QK norm/RoPE/KV
     write, then causal prefill attention on the cache it wrote.  Both kernels
-    are a few microseconds, so each is timed over n back-to-back launches."""
+    are a few microseconds, so each is timed over n launches back to back from
+    a captured graph (no host cost between them)."""
     hq, hkv, S = 16, 8, 512
     q = torch.randn((S, hq, D), device="cuda", generator=gen).half()
     k = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
@@ -654,14 +686,15 @@ def bench_prefill_c1(torch, ga, gen, n: int = 200):
     ga.qk_norm_rope_kv_prefill(q, k, v, qw, kw, inv, qo, kc, vc, EPS, 0)
     ga.attend_prefill(qo, kc, vc, out, 0)
     L = ga.lib()
-    st = torch.cuda.current_stream().cuda_stream
+    cur = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     nargs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), qw.data_ptr(), kw.data_ptr(),
              inv.data_ptr(), qo.data_ptr(), kc.data_ptr(), vc.data_ptr(), EPS, 0, S, hq, hkv, D,
-             S, st)
+             S)
     pargs = (qo.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), 1.0 / math.sqrt(D),
-             hq, hkv, D, S, S, 0, S, st)
-    norm_ms = time_back_to_back(torch, lambda: L.grout_qk_norm_rope_kv_prefill(*nargs), n, 20)
-    attn_ms = time_back_to_back(torch, lambda: L.grout_attn_prefill(*pargs), n, 20)
+             hq, hkv, D, S, S, 0, S)
+    gs = torch.cuda.Stream()
+    norm_ms = time_graph_cycle(torch, lambda: L.grout_qk_norm_rope_kv_prefill(*nargs, cur()), 50, n, gs)
+    attn_ms = time_graph_cycle(torch, lambda: L.grout_attn_prefill(*pargs, cur()), 50, n, gs)
     assert torch.isfinite(out).all().item(), "non-finite c1 output"
     flops = prefill_flops(hq, S)
     nb = norm_bytes(hq, hkv, S)
