@@ -39,7 +39,7 @@ __all__ = [
     "GroutError", "LibraryMissing", "lib", "build_inv_freq", "qk_norm_rope_kv_prefill",
     "qk_norm_rope_kv_decode", "attend_prefill", "fmha_decode_gqa_split",
     "splitk_reduce_merge", "decode_fused", "attend_prefill_split", "prefill_split_scratch",
-    "prefill_splitk_reduce_merge", "add_rms_norm_decode", "gemv_f16", "argmax_scratch",
+    "prefill_splitk_reduce_merge", "add_rms_norm_decode", "gemv_f16", "gemv_silu_mul", "argmax_scratch",
     "argmax_f16", "embed_rms_norm_decode", "silu_mul", "Qwen3DecodeRunner", "QWEN3_LAYER_KEYS",
     "decode_scratch", "decode_counters",
     "pick_num_splits", "DecodeGraphRunner",
@@ -324,6 +324,22 @@ def gemv_f16(weight, x, out):
     for t, nm in ((weight, "weight"), (x, "x"), (out, "out")):
         _f16(t, nm)
     _check(lib().grout_gemv_f16(_ptr(weight), _ptr(x), _ptr(out), m, k, _stream()), "gemv_f16")
+    return out
+
+
+def gemv_silu_mul(gate_up, x, out):
+    """The gate_up GEMV and silu_mul_2d_f16 of the decode graph (src/model.rs:3529-3535,
+    3556-3565) in one launch: out[n] = silu(gate) * up of the f16 rows of gate_up[2n, k] @ x,
+    bit-identical to gemv_f16 followed by silu_mul."""
+    _ensure(gate_up.dim() == 2 and gate_up.shape[0] % 2 == 0,
+            f"gate_up must be [2n, k], got {list(gate_up.shape)}")
+    m2, k = gate_up.shape
+    _ensure(x.numel() == k, f"x must have {k} elements, got {x.numel()}")
+    _ensure(out.numel() == m2 // 2, f"out must have {m2 // 2} elements, got {out.numel()}")
+    for t, nm in ((gate_up, "gate_up"), (x, "x"), (out, "out")):
+        _f16(t, nm)
+    _check(lib().grout_gemv_silu_mul_f16(_ptr(gate_up), _ptr(x), _ptr(out), m2 // 2, k, _stream()),
+           "gemv_silu_mul_f16")
     return out
 
 

@@ -86,6 +86,7 @@ SIGNATURES = {
     "grout_attn_prefill_split_lse_bytes": (c_i64, [c_i32] * 5),
     "grout_add_rms_norm_decode": (c_i32, [c_vp] * 5 + [c_f32, c_i32, c_vp]),
     "grout_gemv_f16": (c_i32, [c_vp] * 3 + [c_i32] * 2 + [c_vp]),
+    "grout_gemv_silu_mul_f16": (c_i32, [c_vp] * 3 + [c_i32] * 2 + [c_vp]),
     "grout_argmax_blocks": (c_i32, [c_i32]),
     "grout_argmax_f16": (c_i32, [c_vp] * 4 + [c_i32, c_vp]),
     "grout_embed_rms_norm_decode": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32,

@@ -105,22 +105,31 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_decode_kernel(
 constexpr int kPointwiseThreads = 256;
 
 // silu_mul_2d_f16 (src/kernels.rs:271-301): out = f16(sigmoid(g) * g * u) in
-// f32 with sigmoid(g) = 1 / (1 + exp(-g)); 8 elements per thread.
+// f32 with sigmoid(g) = 1 / (1 + exp(-g)), for f16 inputs g and u.
+__device__ __forceinline__ half_t silu_mul1(half_t g16, half_t u16) {
+#pragma clang fp contract(off)
+    const float g = static_cast<float>(g16);
+    const float sig = 1.0f / (1.0f + expf(-g));
+    float p = (sig * g) * static_cast<float>(u16);
+    // The product is rounded to f32, then to f16, as the reference computes
+    // it: the empty asm keeps the backend from folding the multiply and the
+    // conversion into one v_fma_mixlo_f16 (a single rounding, 1 ulp away in
+    // rare cases).
+    asm volatile("" : "+v"(p));
+    return static_cast<half_t>(p);
+}
+
+// 8 elements per thread.
 __global__ __launch_bounds__(kPointwiseThreads) void silu_mul_kernel(
     const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, uint16_t* __restrict__ out,
     int n) {
-#pragma clang fp contract(off)
     const int i = (static_cast<int>(blockIdx.x) * kPointwiseThreads + static_cast<int>(threadIdx.x)) * 8;
     if (i >= n) return;
     const half8_t g8 = load_half8(gate + i);
     const half8_t u8 = load_half8(up + i);
     half8_t o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float g = static_cast<float>(g8[e]);
-        const float sig = 1.0f / (1.0f + expf(-g));
-        o[e] = static_cast<half_t>((sig * g) * static_cast<float>(u8[e]));
-    }
+    for (int e = 0; e < 8; ++e) o[e] = silu_mul1(g8[e], u8[e]);
     store_half8(out + i, o);
 }
 
@@ -164,7 +173,12 @@ __device__ __forceinline__ float wave_multi_sum(float (&v)[R], int lane) {
     return v[0];
 }
 
-// Workgroup b computes out rows b*R + [0, R).  Thread t of the workgroup
+// Workgroup b computes out rows b*R + [0, R).  kSilu (the gate_up GEMV with
+// SiLU * up in its epilogue): workgroup b computes gate rows b*R/2 + [0, R/2)
+// and the matching up rows half_m + b*R/2 + [0, R/2) as its R rows, rounds
+// each sum to f16 as the plain GEMV stores it, and writes f16(silu(g) * u)
+// for its R/2 outputs: bit-identical to the GEMV followed by silu_mul_kernel,
+// without the second launch and the intermediate's round trip.  Thread t of the workgroup
 // reads the 16-byte chunks t, t + 256, ... of each of the R rows (4 KB of a
 // row per workgroup load step, contiguous), so a row of k halves is streamed
 // by all 256 threads at once and R * kGemvUnroll chunks per thread are in
@@ -172,21 +186,25 @@ __device__ __forceinline__ float wave_multi_sum(float (&v)[R], int lane) {
 // every workgroup hits it in L2).  Products are exact in f32
 // (v_dot2_f32_f16); the sum order is per thread, then across lanes, then
 // across the four wavefronts.
-template <int R>
+template <int R, bool kSilu = false>
 __global__ __launch_bounds__(kGemvThreads) void gemv_f16_kernel(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, uint16_t* __restrict__ out,
-    int m, int k) {
+    int m, int k, int half_m = 0) {
+    static_assert(!kSilu || R >= 2, "a SiLU workgroup pairs R/2 gate rows with R/2 up rows");
     __shared__ float red[kGemvThreads / kWave][R];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
     const int nchunk = k / 8;
-    const int row0 = static_cast<int>(blockIdx.x) * R;
+    constexpr int kOut = kSilu ? R / 2 : R;  // outputs per workgroup
+    const int row0 = static_cast<int>(blockIdx.x) * kOut;
     const half8_t* xc = reinterpret_cast<const half8_t*>(x);
     const half8_t* wr[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int row = min(row0 + r, m - 1);  // rows past m repeat the last (not stored)
+        // Outputs past m repeat the last row (not stored).
+        const int o = min(row0 + r % kOut, m - 1);
+        const int row = (kSilu && r >= kOut) ? half_m + o : o;
         wr[r] = reinterpret_cast<const half8_t*>(W + static_cast<int64_t>(row) * k);
     }
     float acc[R];
@@ -219,7 +237,18 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_f16_kernel(
     constexpr int kStride = kWave / R;
     if (lane % kStride == 0) red[wave][lane / kStride] = v;
     __syncthreads();
-    if (tid < R && row0 + tid < m) {
+    if constexpr (kSilu) {
+        if (tid < kOut && row0 + tid < m) {
+            float tg = red[0][tid], tu = red[0][tid + kOut];
+#pragma unroll
+            for (int w = 1; w < kGemvThreads / kWave; ++w) {
+                tg += red[w][tid];
+                tu += red[w][tid + kOut];
+            }
+            out[row0 + tid] = __builtin_bit_cast(
+                uint16_t, silu_mul1(static_cast<half_t>(tg), static_cast<half_t>(tu)));
+        }
+    } else if (tid < R && row0 + tid < m) {
         float t = red[0][tid];
 #pragma unroll
         for (int w = 1; w < kGemvThreads / kWave; ++w) t += red[w][tid];
@@ -363,6 +392,27 @@ extern "C" int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uin
         case 4: hipLaunchKernelGGL(gemv_f16_kernel<4>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
         case 2: hipLaunchKernelGGL(gemv_f16_kernel<2>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
         default: hipLaunchKernelGGL(gemv_f16_kernel<1>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
+    }
+    return launch_status();
+}
+
+extern "C" int32_t grout_gemv_silu_mul_f16(const uint16_t* gate_up, const uint16_t* x, uint16_t* out,
+                                           int32_t n, int32_t k, grout_stream_t stream) {
+    GROUT_REQUIRE_PTR(gate_up);
+    GROUT_REQUIRE_PTR(x);
+    GROUT_REQUIRE(out != nullptr, GROUT_ERR_NULL_POINTER);
+    GROUT_REQUIRE((reinterpret_cast<uintptr_t>(out) & 1u) == 0, GROUT_ERR_ALIGNMENT);
+    GROUT_REQUIRE(n >= 1 && n <= (1 << 29) && k >= 8 && k % 8 == 0 && k <= kGemvMaxK, GROUT_ERR_ARG);
+    // Weight rows per workgroup as grout_gemv_f16 picks them for the 2n rows.
+    const int rows = 2 * n >= 8 * 1024 ? 8 : 2 * n >= 4 * 1024 ? 4 : 2;
+    const int outs = rows / 2;
+    const unsigned blocks = static_cast<unsigned>((n + outs - 1) / outs);
+    const hipStream_t s = to_hip(stream);
+    const dim3 block(kGemvThreads);
+    switch (rows) {
+        case 8: hipLaunchKernelGGL((gemv_f16_kernel<8, true>), dim3(blocks), block, 0, s, gate_up, x, out, n, k, n); break;
+        case 4: hipLaunchKernelGGL((gemv_f16_kernel<4, true>), dim3(blocks), block, 0, s, gate_up, x, out, n, k, n); break;
+        default: hipLaunchKernelGGL((gemv_f16_kernel<2, true>), dim3(blocks), block, 0, s, gate_up, x, out, n, k, n); break;
     }
     return launch_status();
 }

@@ -5,7 +5,7 @@
 // Per replay: embedding + input RMSNorm of the token the previous replay
 // picked; for each layer [add + input RMSNorm] -> qkv GEMV -> fused QK
 // norm/RoPE/KV write + split-K decode + merge -> o_proj GEMV -> add +
-// post-attention RMSNorm -> gate_up GEMV -> SiLU * up -> down GEMV; then the
+// post-attention RMSNorm -> gate_up GEMV with SiLU * up -> down GEMV; then the
 // final add + RMSNorm, the lm_head GEMV and the greedy argmax, which writes
 // the next token where the embedding reads it.  The last layer's attention
 // advances the device position, so consecutive replays need no host writes.
@@ -26,8 +26,7 @@ namespace {
 // Device workspace carved into the step's activations and scratch; every
 // buffer starts on a 256-byte boundary.
 struct Qwen3Workspace {
-    int64_t hidden, hidden_after_attn, normed, qkv, q_out, attn_out, attn_proj, gate_up, ff,
-        ff_down, att_partial, lse_partial, counters, block_max, block_idx, total;
+    int64_t hidden, hidden_after_attn, normed, qkv, q_out, attn_out, attn_proj, ff, ff_down, att_partial, lse_partial, counters, block_max, block_idx, total;
 };
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t{255}; }
@@ -70,7 +69,6 @@ int32_t layout(const grout_qwen3_model& M, Qwen3Workspace* w) {
     w->q_out = take(2 * d * (M.num_q_heads + M.num_kv_heads));
     w->attn_out = take(2 * d * M.num_q_heads);
     w->attn_proj = take(h2);
-    w->gate_up = take(int64_t{4} * M.intermediate);
     w->ff = take(int64_t{2} * M.intermediate);
     w->ff_down = take(h2);
     w->att_partial = take(partial);
@@ -123,7 +121,6 @@ extern "C" int32_t grout_qwen3_decode_step(const grout_qwen3_model* model,
     uint16_t* q_out = at<uint16_t>(ws, w.q_out);
     uint16_t* attn_out = at<uint16_t>(ws, w.attn_out);
     uint16_t* attn_proj = at<uint16_t>(ws, w.attn_proj);
-    uint16_t* gate_up = at<uint16_t>(ws, w.gate_up);
     uint16_t* ff = at<uint16_t>(ws, w.ff);
     uint16_t* ff_down = at<uint16_t>(ws, w.ff_down);
     uint16_t* att_partial = at<uint16_t>(ws, w.att_partial);
@@ -157,10 +154,9 @@ extern "C" int32_t grout_qwen3_decode_step(const grout_qwen3_model* model,
         st = grout_add_rms_norm_decode(hidden, attn_proj, L.post_attn_norm, normed,
                                        hidden_after_attn, M.eps, M.hidden, stream);
         if (st != GROUT_OK) break;  // :3513-3526
-        st = grout_gemv_f16(L.gate_up_proj, normed, gate_up, 2 * M.intermediate, M.hidden, stream);
-        if (st != GROUT_OK) break;  // :3529-3535
-        st = grout_silu_mul_f16(gate_up, gate_up + M.intermediate, ff, M.intermediate, stream);
-        if (st != GROUT_OK) break;  // :3556-3565
+        // :3529-3535 gate_up GEMV and :3556-3565 SiLU * up, in one launch.
+        st = grout_gemv_silu_mul_f16(L.gate_up_proj, normed, ff, M.intermediate, M.hidden, stream);
+        if (st != GROUT_OK) break;
         st = grout_gemv_f16(L.down_proj, ff, ff_down, M.hidden, M.intermediate, stream);
     }                               // :3568-3574
     if (st != GROUT_OK) return st;

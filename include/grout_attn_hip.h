@@ -250,6 +250,15 @@ int32_t grout_silu_mul_f16(const uint16_t* gate, const uint16_t* up, uint16_t* o
 int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uint16_t* out, int32_t m,
                        int32_t k, grout_stream_t stream);
 
+/* The decode graph's gate_up GemvInPlace node followed by silu_mul_2d_f16
+ * (src/model.rs:3529-3535, 3556-3565) in one launch; the reference records two
+ * ops.  gate_up is the merged [2n, k] weight (gate rows [0, n), up rows
+ * [n, 2n)); out[i] = grout_silu_mul_f16 of the f16 rows i and n + i of
+ * grout_gemv_f16(gate_up, x), bit for bit, without the [2n] intermediate.
+ * n at most 2^29; k and alignment as grout_gemv_f16. */
+int32_t grout_gemv_silu_mul_f16(const uint16_t* gate_up, const uint16_t* x, uint16_t* out,
+                                int32_t n, int32_t k, grout_stream_t stream);
+
 /* Replaces argmax_blocks_f16 + argmax_reduce_blocks_to_u32 (src/kernels.rs:345-392,
  * 458-505), the in-graph greedy token pick: *token = the lowest index of the
  * largest f32(logits[i]) over [0, n) (NaN logits are never picked).

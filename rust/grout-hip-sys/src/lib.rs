@@ -219,6 +219,9 @@ extern "C" {
     pub fn grout_gemv_f16(
         weight: *const u16, x: *const u16, out: *mut u16, m: i32, k: i32, stream: HipStream,
     ) -> i32;
+    pub fn grout_gemv_silu_mul_f16(
+        gate_up: *const u16, x: *const u16, out: *mut u16, n: i32, k: i32, stream: HipStream,
+    ) -> i32;
     pub fn grout_argmax_blocks(n: i32) -> i32;
     pub fn grout_argmax_f16(
         logits: *const u16, block_max: *mut f32, block_idx: *mut u32, token: *mut u32, n: i32,

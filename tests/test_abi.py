@@ -286,6 +286,17 @@ def test_token_step_op_checks(L):
     assert s(A, A, U, 64, S) == -2
     assert s(A, A, A, 12, S) == -9
     assert s(A, A, A, 0, S) == -9
+    gs = L.grout_gemv_silu_mul_f16
+    # gate_up, x, out, n, k, stream
+    assert gs(0, A, A, 8, 8, S) == -1
+    assert gs(A, 0, A, 8, 8, S) == -1
+    assert gs(A, A, 0, 8, 8, S) == -1
+    assert gs(U, A, A, 8, 8, S) == -2
+    assert gs(A, A, A + 1, 8, 8, S) == -2                 # out needs 2-byte alignment only
+    assert gs(A, A, A, 0, 8, S) == -9
+    assert gs(A, A, A, (1 << 29) + 1, 8, S) == -9
+    assert gs(A, A, A, 8, 12, S) == -9
+    assert gs(A, A, A, 8, 32776, S) == -9
 
 
 def test_cast_checks(L):
@@ -323,7 +334,7 @@ def test_token_step_runner_checks(L):
     ws = L.grout_qwen3_workspace_bytes
     assert ws(None) == -1
     n = ws(_qwen3_model())
-    # hidden x3 + qkv + q_out + attn_out + attn_proj + gate_up + ff + ff_down
+    # hidden x3 + qkv + q_out + attn_out + attn_proj + ff + ff_down
     # + partials + lse + counters + argmax blocks, each rounded up to 256 bytes.
     assert n > 2 * (3 * 256 + 8 * 128 + 6 * 128 + 4 * 128 + 256 + 1024 + 512 + 256)
     assert n % 256 == 0

@@ -64,6 +64,39 @@ def test_silu_mul_matches_oracle(gpu, n):
     assert f16_ulp_diff(out.cpu().numpy(), oracle.silu_mul(gate, up)).max() <= 1
 
 
+@pytest.mark.parametrize("n,k,seed", [
+    (25600, 5120, 1),   # Qwen3-32B intermediate / hidden: 8 weight rows per workgroup
+    (9728, 2560, 2),    # Qwen3-4B intermediate / hidden
+    (3000, 1032, 3),    # 6000 weight rows: 4 per workgroup; k not a whole unrolled chunk row
+    (1001, 24, 4),      # 2002 rows: 2 per workgroup, the last one half full
+    (1, 8, 5),          # one output, one chunk
+])
+def test_gemv_silu_mul_equals_two_launches(gpu, n, k, seed):
+    """grout_gemv_silu_mul_f16 (the gate_up GEMV with SiLU * up in its epilogue, the
+    token step's form) equals grout_gemv_f16 followed by grout_silu_mul_f16, bit for
+    bit; both of those are held to the oracle by their own tests."""
+    import torch
+    import grout_amd
+
+    g = rng(1450 + seed)
+    w = normal_f16(g, (2 * n, k), 1.0 / np.sqrt(k))
+    w[:4] *= np.float16(40.0)  # large gate values: silu saturates (g -> g, -> -0)
+    x = normal_f16(g, k)
+    dw, dx = _dev(torch, w), _dev(torch, x)
+    gu = torch.empty((2 * n,), dtype=torch.float16, device="cuda")
+    grout_amd.gemv_f16(dw, dx, gu)
+    n8 = -(-n // 8) * 8  # silu_mul takes whole 16-byte chunks: pad with zeros
+    gate = torch.zeros((n8,), dtype=torch.float16, device="cuda")
+    up = torch.zeros_like(gate)
+    gate[:n], up[:n] = gu[:n], gu[n:]
+    ref = torch.empty_like(gate)
+    grout_amd.silu_mul(gate, up, ref)
+    out = torch.full((n,), float("nan"), dtype=torch.float16, device="cuda")
+    grout_amd.gemv_silu_mul(dw, dx, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref[:n].view(torch.int16))
+
+
 def _device_model(torch, m):
     layers = [{k: _dev(torch, v) for k, v in L.items()} for L in m["layers"]]
     return dict(layers=layers, embed_tokens=_dev(torch, m["embed_tokens"]),
