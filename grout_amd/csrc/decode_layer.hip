@@ -374,6 +374,18 @@ extern "C" int32_t grout_silu_mul_f16(const uint16_t* gate, const uint16_t* up, 
     return launch_status();
 }
 
+// Residency of the largest GEMVs.  Their launches reserve unused LDS so that at
+// most kGemvResidentBig (plain GEMV of >= 2^28 weight elements: lm_head) or
+// kGemvResidentSilu (the gate_up GEMV with SiLU * up) workgroups share a CU:
+// fewer concurrent row streams per CU.  Measured in the Qwen3-32B token step
+// (one process, graphs alternating): 12.670 -> 12.592 ms/token with 2 and 3;
+// capping every GEMV, or these at 4 or 6, measured no gain.
+constexpr int kGemvResidentBig = 2;
+constexpr int kGemvResidentSilu = 3;
+constexpr size_t gemv_reserve_lds(int resident) {
+    return static_cast<size_t>(160 * 1024 / resident - 1024);  // static LDS stays below 1 KB
+}
+
 extern "C" int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uint16_t* out,
                                   int32_t m, int32_t k, grout_stream_t stream) {
     GROUT_REQUIRE_PTR(weight);
@@ -387,8 +399,9 @@ extern "C" int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uin
     const unsigned blocks = static_cast<unsigned>((m + rows - 1) / rows);
     const hipStream_t s = to_hip(stream);
     const dim3 block(kGemvThreads);
+    const size_t lds = static_cast<int64_t>(m) * k >= (int64_t{1} << 28) ? gemv_reserve_lds(kGemvResidentBig) : 0;
     switch (rows) {
-        case 8: hipLaunchKernelGGL(gemv_f16_kernel<8>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
+        case 8: hipLaunchKernelGGL(gemv_f16_kernel<8>, dim3(blocks), block, lds, s, weight, x, out, m, k); break;
         case 4: hipLaunchKernelGGL(gemv_f16_kernel<4>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
         case 2: hipLaunchKernelGGL(gemv_f16_kernel<2>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
         default: hipLaunchKernelGGL(gemv_f16_kernel<1>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
@@ -410,7 +423,8 @@ extern "C" int32_t grout_gemv_silu_mul_f16(const uint16_t* gate_up, const uint16
     const hipStream_t s = to_hip(stream);
     const dim3 block(kGemvThreads);
     switch (rows) {
-        case 8: hipLaunchKernelGGL((gemv_f16_kernel<8, true>), dim3(blocks), block, 0, s, gate_up, x, out, n, k, n); break;
+        case 8: hipLaunchKernelGGL((gemv_f16_kernel<8, true>), dim3(blocks), block,
+                                   gemv_reserve_lds(kGemvResidentSilu), s, gate_up, x, out, n, k, n); break;
         case 4: hipLaunchKernelGGL((gemv_f16_kernel<4, true>), dim3(blocks), block, 0, s, gate_up, x, out, n, k, n); break;
         default: hipLaunchKernelGGL((gemv_f16_kernel<2, true>), dim3(blocks), block, 0, s, gate_up, x, out, n, k, n); break;
     }
