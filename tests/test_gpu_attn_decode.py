@@ -226,6 +226,7 @@ def _fused_case(seed, hq, hkv, MS):
     (64, 4, 3000, 3100, 40, 77),   # G = 16: batches of 32 (32 + 8)
     (48, 4, 4000, 4100, 100, 78),  # G = 12: batches of 42 (42 + 42 + 16)
     (8, 1, 3000, 3100, 128, 86),   # one KV head (MQA-style), G = 8: 2 batches of 64 splits
+    (64, 8, 131071, 131072, 32, 87),  # 128K context, the last slot: 4096-token splits
     (64, 4, 5000, 5100, 64, 79),   # G = 16: 32 + 32 (4 KV heads' picked split count)
     # One batch, LSE block copied first.
     (64, 8, 3000, 3100, 48, 80),   # G = 8, 48 splits: two weight slots per lane
