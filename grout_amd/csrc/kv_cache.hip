@@ -8,24 +8,36 @@
 //   new_k/new_v [seq_len, num_kv_heads, head_dim] f16, contiguous;
 //   k_cache/v_cache [num_kv_heads, max_seq_len, head_dim] f16.
 // HBM-bound copy: every thread moves one 16-byte (or, for head_dim % 8 != 0,
-// 8-byte) unit of K and the same unit of V; consecutive threads read
-// consecutive source bytes and write within one cache row.
+// 8-byte) unit of K and the same unit of V; consecutive threads cover one
+// head's rows of a 16-token tile, so the cache side is written in long
+// contiguous runs.
 #include "abi_util.h"
 #include "common.h"
 
 namespace grout {
 
+// Tokens per tile.  Lane i enumerates [token tile][head][token in tile][unit],
+// so the 256 lanes of a workgroup (head_dim 128: 16 tokens x 16 units) write
+// one head's 16 consecutive cache rows, 4 KB contiguous, and read 256-byte
+// rows 2 KB apart that the neighbouring workgroups (the other heads of the
+// tile) read beside them.  Row-major lanes wrote 512-byte pieces of eight
+// heads per workgroup, 8-13% slower.
+constexpr int kKvTileTokens = 16;
+
 template <typename Unit, bool kDevicePos>
 __global__ __launch_bounds__(256) void kv_cache_update_kernel(
     const Unit* __restrict__ new_k, const Unit* __restrict__ new_v, Unit* __restrict__ k_cache,
     Unit* __restrict__ v_cache, int position_start, const uint32_t* __restrict__ d_position,
-    int64_t total_units, int units_per_row, int num_kv_heads, int max_seq_len) {
+    int64_t total_units, int units_per_row, int num_kv_heads, int max_seq_len, int seq_len) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= total_units) return;
     const int u = static_cast<int>(i % units_per_row);
-    const int64_t rh = i / units_per_row;  // = s * num_kv_heads + h
-    const int h = static_cast<int>(rh % num_kv_heads);
-    const int64_t s = rh / num_kv_heads;
+    const int64_t r = i / units_per_row;
+    const int t_in = static_cast<int>(r % kKvTileTokens);
+    const int64_t ht = r / kKvTileTokens;  // = tile * num_kv_heads + h
+    const int h = static_cast<int>(ht % num_kv_heads);
+    const int64_t s = (ht / num_kv_heads) * kKvTileTokens + t_in;
+    if (s >= seq_len) return;  // the last tile is ragged
     int64_t pos;
     if constexpr (kDevicePos) {
         pos = static_cast<int64_t>(*d_position) + s;
@@ -33,9 +45,14 @@ __global__ __launch_bounds__(256) void kv_cache_update_kernel(
     } else {
         pos = position_start + s;
     }
+    const int64_t src = (s * num_kv_heads + h) * units_per_row + u;
     const int64_t dst = (static_cast<int64_t>(h) * max_seq_len + pos) * units_per_row + u;
-    k_cache[dst] = new_k[i];
-    v_cache[dst] = new_v[i];
+    // Non-temporal stores: the rows are not read again by this kernel, and
+    // streaming them past the caches measured 8% faster with the data in HBM
+    // and 13% faster with it in the last-level cache.  (Non-temporal loads
+    // lose whenever the new rows are still cached from their producer.)
+    __builtin_nontemporal_store(new_k[src], k_cache + dst);
+    __builtin_nontemporal_store(new_v[src], v_cache + dst);
 }
 
 template <bool kDevicePos>
@@ -46,7 +63,8 @@ static int32_t launch_kv_update(const uint16_t* new_k, const uint16_t* new_v, ui
                                 hipStream_t stream) {
     const bool wide = head_dim % 8 == 0;
     const int units_per_row = wide ? head_dim / 8 : head_dim / 4;
-    const int64_t total = static_cast<int64_t>(seq_len) * num_kv_heads * units_per_row;
+    const int64_t tiles = (static_cast<int64_t>(seq_len) + kKvTileTokens - 1) / kKvTileTokens;
+    const int64_t total = tiles * kKvTileTokens * num_kv_heads * units_per_row;
     if (total == 0) return GROUT_OK;
     const int64_t blocks = (total + 255) / 256;
     if (blocks > 0x7fffffff) return GROUT_ERR_SEQ_RANGE;
@@ -55,14 +73,14 @@ static int32_t launch_kv_update(const uint16_t* new_k, const uint16_t* new_v, ui
                            dim3(256), 0, stream, reinterpret_cast<const uint4_t*>(new_k),
                            reinterpret_cast<const uint4_t*>(new_v), reinterpret_cast<uint4_t*>(k_cache),
                            reinterpret_cast<uint4_t*>(v_cache), position_start, d_position, total,
-                           units_per_row, num_kv_heads, max_seq_len);
+                           units_per_row, num_kv_heads, max_seq_len, seq_len);
     } else {
         typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
         hipLaunchKernelGGL((kv_cache_update_kernel<uint2_t, kDevicePos>), dim3(static_cast<unsigned>(blocks)),
                            dim3(256), 0, stream, reinterpret_cast<const uint2_t*>(new_k),
                            reinterpret_cast<const uint2_t*>(new_v), reinterpret_cast<uint2_t*>(k_cache),
                            reinterpret_cast<uint2_t*>(v_cache), position_start, d_position, total,
-                           units_per_row, num_kv_heads, max_seq_len);
+                           units_per_row, num_kv_heads, max_seq_len, seq_len);
     }
     return launch_status();
 }

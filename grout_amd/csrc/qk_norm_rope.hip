@@ -24,6 +24,30 @@ namespace grout {
 constexpr int kNormThreads = 256;
 constexpr int kNormRowSlots = kNormThreads / 8;  // rows in flight per workgroup
 constexpr int kNormMaxTokens = 8;                // tokens per workgroup (LDS sin/cos table)
+// Prefill launches reserve dynamic LDS so that at most kNormResident
+// workgroups (16 waves) share a CU instead of the 8 that registers and the
+// static 4 KB table allow: fewer concurrent row streams per CU measured
+// 1.5-3% faster at 8192-32768 tokens (c3: 33.2 -> 32.5 us) and no different
+// on grids of at most 4 workgroups per CU.
+constexpr int kNormResident = 4;
+constexpr size_t kNormReserveLds =
+    160 * 1024 / kNormResident - 2 * kNormMaxTokens * 64 * sizeof(float) - 1024;
+
+// Output stores of the prefill form are non-temporal: q_out and the cache rows
+// are not read again by this kernel, and streaming them past the caches
+// measured 7% faster with the data in HBM (41.3 -> 38.4 us at c3) and no
+// slower with it in the last-level cache.  The decode form keeps ordinary
+// stores: the attention launch that follows reads its rows at once.
+// (Non-temporal loads lose whenever the inputs are still cached from their
+// producer.)
+template <bool kNonTemporal>
+__device__ __forceinline__ void store_out8(uint16_t* p, half8_t v) {
+    if constexpr (kNonTemporal) {
+        __builtin_nontemporal_store(v, reinterpret_cast<half8_t*>(p));
+    } else {
+        store_half8(p, v);
+    }
+}
 
 template <bool kDevicePos>
 __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_kv_kernel(
@@ -106,15 +130,15 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_kv_kernel(
 
         if (is_q) {
             uint16_t* dst = q_out + (static_cast<int64_t>(s) * num_q_heads + h) * kHeadDim;
-            store_half8(dst + 8 * lane8, ylo);
-            store_half8(dst + 64 + 8 * lane8, yhi);
+            store_out8<!kDevicePos>(dst + 8 * lane8, ylo);
+            store_out8<!kDevicePos>(dst + 64 + 8 * lane8, yhi);
         } else if (static_cast<unsigned>(pos) < static_cast<unsigned>(max_seq_len)) {
             const int64_t slot = (static_cast<int64_t>(kvh) * max_seq_len + pos) * kHeadDim;
-            store_half8(k_cache + slot + 8 * lane8, ylo);
-            store_half8(k_cache + slot + 64 + 8 * lane8, yhi);
+            store_out8<!kDevicePos>(k_cache + slot + 8 * lane8, ylo);
+            store_out8<!kDevicePos>(k_cache + slot + 64 + 8 * lane8, yhi);
             const uint16_t* vsrc = v + (static_cast<int64_t>(s) * num_kv_heads + kvh) * kHeadDim;
-            store_u128(v_cache + slot + 8 * lane8, load_u128(vsrc + 8 * lane8));
-            store_u128(v_cache + slot + 64 + 8 * lane8, load_u128(vsrc + 64 + 8 * lane8));
+            store_out8<!kDevicePos>(v_cache + slot + 8 * lane8, load_half8(vsrc + 8 * lane8));
+            store_out8<!kDevicePos>(v_cache + slot + 64 + 8 * lane8, load_half8(vsrc + 64 + 8 * lane8));
         }
     }
 }
@@ -166,7 +190,8 @@ extern "C" int32_t grout_qk_norm_rope_kv_prefill(
     const int heads = num_q_heads + num_kv_heads;
     norm_launch_shape(seq_len, heads, &tpb, &hpb);
     dim3 grid((seq_len + tpb - 1) / tpb, (heads + hpb - 1) / hpb);
-    hipLaunchKernelGGL(qk_norm_rope_kv_kernel<false>, grid, dim3(kNormThreads), 0, to_hip(stream),
+    hipLaunchKernelGGL(qk_norm_rope_kv_kernel<false>, grid, dim3(kNormThreads), kNormReserveLds,
+                       to_hip(stream),
                        q, k, v, q_weight, k_weight, inv_freq, q_out, k_cache, v_cache, eps,
                        position_start, static_cast<const uint32_t*>(nullptr), seq_len,
                        num_q_heads, num_kv_heads, max_seq_len, tpb, hpb);
