@@ -338,16 +338,18 @@ def bench_prefill_split(torch, ga, pre, steps, num_splits=4, block_m=128, block_
 
 
 def bench_norm(torch, ga, steps, warmup, gen):
-    """qk_norm_rope_kv_prefill at c3 shapes (201.3 MB per launch).  `ms`: back to back
-    on one set of buffers, which the 256 MB last-level cache partly serves between
-    launches.  `cold_ms`: launches cycling over three sets (604 MB), so every launch
-    streams its inputs and outputs from and to HBM."""
+    """qk_norm_rope_kv_prefill at c3 shapes (201.3 MB per launch), launches issued from
+    a captured graph (no host cost between them).  `ms`: one set of buffers, which the
+    256 MB last-level cache partly serves between launches.  `cold_ms`: launches
+    cycling over four sets (805 MB; 384 MB of inputs, as the non-temporal output
+    stores do not stay in that cache), so every launch streams its inputs and outputs
+    from and to HBM."""
     hq, hkv, S = 32, 8, 8192
     qw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
     kw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()
     inv = ga.build_inv_freq(THETA).cuda()
     sets = []
-    for _ in range(3):
+    for _ in range(4):
         q = torch.randn((S, hq, D), device="cuda", generator=gen).half()
         k = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
         v = torch.randn((S, hkv, D), device="cuda", generator=gen).half()
@@ -357,15 +359,16 @@ def bench_norm(torch, ga, steps, warmup, gen):
     ga.qk_norm_rope_kv_prefill(q, k, v, qw, kw, inv, out, kc, vc, EPS, 0)  # mirror checks once
     # Through the C entry point, like the other short kernels' legs.
     L = ga.lib()
-    st = torch.cuda.current_stream().cuda_stream
+    gs = torch.cuda.Stream()
     calls = [(q.data_ptr(), k.data_ptr(), v.data_ptr(), qw.data_ptr(), kw.data_ptr(),
               inv.data_ptr(), o.data_ptr(), c.data_ptr(), w.data_ptr(), EPS, 0, S, hq, hkv, D,
-              S, st) for q, k, v, o, c, w in sets]
+              S, gs.cuda_stream) for q, k, v, o, c, w in sets]
+    torch.cuda.synchronize()
     fn = lambda: L.grout_qk_norm_rope_kv_prefill(*calls[0])  # noqa: E731
-    ms = time_back_to_back(torch, fn, max(steps, 50), warmup)
+    ms = time_graph_cycle(torch, fn, 12, max(steps, 60), gs)
     it = itertools.cycle(calls)
     cfn = lambda: L.grout_qk_norm_rope_kv_prefill(*next(it))  # noqa: E731
-    cold_ms = time_back_to_back(torch, cfn, 3 * max(steps, 17), warmup)
+    cold_ms = time_graph_cycle(torch, cfn, 12, max(steps, 60), gs)  # 3 passes over the 4 sets
     nb = norm_bytes(hq, hkv, S)
     return dict(ms=ms, bytes=nb, gbs=nb / (ms * 1e-3) / 1e9, cold_ms=cold_ms,
                 cold_gbs=nb / (cold_ms * 1e-3) / 1e9)
@@ -373,9 +376,11 @@ def bench_norm(torch, ga, steps, warmup, gen):
 
 def bench_kv_update(torch, ga, steps, warmup, gen):
     """kv_cache_update_seq at c3 shapes: 8192 rows x 8 KV heads of K and V into
-    a [8, 8192, 128] cache (read 33.6 MB, write 33.6 MB).  `ms`: back to back on
-    one set of buffers (last-level cache resident); `cold_ms`: cycling over ten
-    sets (671 MB), every launch from and to HBM."""
+    a [8, 8192, 128] cache (read 33.6 MB, write 33.6 MB), launches issued from a
+    captured graph (the ~10 us kernel is close to the host's per-launch cost).
+    `ms`: one set of buffers (last-level cache resident); `cold_ms`: cycling over
+    ten sets (671 MB; 336 MB of inputs, as the non-temporal cache stores do not stay
+    in the 256 MB last-level cache), every launch from and to HBM."""
     hkv, S = 8, 8192
     sets = []
     for _ in range(10):
@@ -384,17 +389,16 @@ def bench_kv_update(torch, ga, steps, warmup, gen):
         kc = torch.zeros((hkv, S, D), device="cuda", dtype=torch.float16)
         sets.append((nk, nv, kc, torch.zeros_like(kc)))
     ga.kv_cache_update_seq(*sets[0], 0)  # argument checks of the Python mirror once
-    # Back to back through the C entry point: the ~12 us kernel outruns the
-    # Python mirror's per-call cost.
     L = ga.lib()
-    st = torch.cuda.current_stream().cuda_stream
-    calls = [(nk.data_ptr(), nv.data_ptr(), kc.data_ptr(), vc.data_ptr(), 0, S, hkv, D, S, st)
-             for nk, nv, kc, vc in sets]
+    gs = torch.cuda.Stream()
+    calls = [(nk.data_ptr(), nv.data_ptr(), kc.data_ptr(), vc.data_ptr(), 0, S, hkv, D, S,
+              gs.cuda_stream) for nk, nv, kc, vc in sets]
+    torch.cuda.synchronize()
     fn = lambda: L.grout_kv_cache_update_seq(*calls[0])  # noqa: E731
-    ms = time_back_to_back(torch, fn, max(steps, 50), warmup)
+    ms = time_graph_cycle(torch, fn, 20, max(steps, 100), gs)
     it = itertools.cycle(calls)
     cfn = lambda: L.grout_kv_cache_update_seq(*next(it))  # noqa: E731
-    cold_ms = time_back_to_back(torch, cfn, 10 * max(steps, 5), warmup)
+    cold_ms = time_graph_cycle(torch, cfn, 20, max(steps, 100), gs)  # 2 passes over the 10 sets
     nb = 2 * 2 * S * hkv * D * 2
     return dict(ms=ms, bytes=nb, gbs=nb / (ms * 1e-3) / 1e9, cold_ms=cold_ms,
                 cold_gbs=nb / (cold_ms * 1e-3) / 1e9)
@@ -664,8 +668,9 @@ def bench_mfma_probe(torch, launches: int = 8):
 
 def bench_hbm_probe(torch, gib: int = 4, launches: int = 5):
     """Sustained HBM read rate of a plain streaming kernel (bench_probes/hbm_read.hip)
-    over a buffer far larger than the 256 MB last-level cache: the practical ceiling of the
-    HBM-bound kernels.  GB/s (1e9 bytes)."""
+    over a buffer far larger than the 256 MB last-level cache, the best of 1, 2 and 4
+    workgroups per CU: the practical ceiling of the HBM-bound kernels.  GB/s (1e9
+    bytes)."""
     import ctypes
 
     import bench_probes
@@ -676,22 +681,67 @@ def bench_hbm_probe(torch, gib: int = 4, launches: int = 5):
     fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
     nbytes = gib << 30
     src = torch.empty((nbytes,), dtype=torch.uint8, device="cuda").fill_(1)
-    blocks = 8 * torch.cuda.get_device_properties(0).multi_processor_count
-    out = torch.empty((blocks * 256,), dtype=torch.int32, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty((4 * cus * 256,), dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream()
-    for _ in range(2):
-        assert fn(src.data_ptr(), nbytes, out.data_ptr(), blocks, stream.cuda_stream) == 0
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for _ in range(launches):
-        assert fn(src.data_ptr(), nbytes, out.data_ptr(), blocks, stream.cuda_stream) == 0
-    b.record(stream)
-    torch.cuda.synchronize()
-    gbs = launches * nbytes / (a.elapsed_time(b) * 1e-3) / 1e9
+    best = None
+    for per_cu in (1, 2, 4):
+        blocks = per_cu * cus
+        for _ in range(2):
+            assert fn(src.data_ptr(), nbytes, out.data_ptr(), blocks, stream.cuda_stream) == 0
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(launches):
+            assert fn(src.data_ptr(), nbytes, out.data_ptr(), blocks, stream.cuda_stream) == 0
+        b.record(stream)
+        torch.cuda.synchronize()
+        gbs = launches * nbytes / (a.elapsed_time(b) * 1e-3) / 1e9
+        if best is None or gbs > best["gbs"]:
+            best = dict(gbs=gbs, bytes=nbytes, blocks=blocks, workgroups_per_cu=per_cu)
     del src
     torch.cuda.empty_cache()
-    return dict(gbs=gbs, bytes=nbytes, blocks=blocks)
+    return best
+
+
+def bench_hbm_copy_probe(torch, gib: int = 2, launches: int = 5):
+    """Sustained rate of a plain streaming copy (bench_probes/hbm_copy.hip), bytes read
+    plus bytes written, over buffers far larger than the 256 MB last-level cache; the
+    best of 4 and 8 workgroups per CU.  The practical ceiling of kernels that read and
+    write HBM in equal parts (the QK norm/RoPE/KV write, the KV-cache suffix writer).
+    GB/s (1e9 bytes)."""
+    import ctypes
+
+    import bench_probes
+
+    lib = ctypes.CDLL(bench_probes.lib_path())
+    fn = lib.grout_probe_hbm_copy
+    fn.restype = ctypes.c_int32
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
+    nbytes = gib << 30
+    src = torch.empty((nbytes,), dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.zeros((nbytes,), dtype=torch.uint8, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = torch.cuda.current_stream()
+    best = None
+    for per_cu in (4, 8):
+        blocks = per_cu * cus
+        for _ in range(2):
+            assert fn(src.data_ptr(), dst.data_ptr(), nbytes, blocks, stream.cuda_stream) == 0
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(launches):
+            assert fn(src.data_ptr(), dst.data_ptr(), nbytes, blocks, stream.cuda_stream) == 0
+        b.record(stream)
+        torch.cuda.synchronize()
+        gbs = launches * 2 * nbytes / (a.elapsed_time(b) * 1e-3) / 1e9
+        if best is None or gbs > best["gbs"]:
+            best = dict(gbs=gbs, bytes=2 * nbytes, blocks=blocks, workgroups_per_cu=per_cu)
+    assert bool(torch.equal(src[: 1 << 20], dst[: 1 << 20])), "copy probe wrote wrong bytes"
+    del src, dst
+    torch.cuda.empty_cache()
+    return best
 
 
 def bench_prefill_c1(torch, ga, gen, n: int = 200):
@@ -1072,7 +1122,11 @@ def main(argv=None) -> int:
                 f"{ts['tokens_per_s']:.1f} tok/s, {ts['gbs']:.0f} GB/s")
         elif args.only == "hbm-probe":
             hp = bench_hbm_probe(torch)
-            log(f"hbm read probe: {hp['gbs']:.0f} GB/s over {hp['bytes'] >> 30} GiB")
+            log(f"hbm read probe: {hp['gbs']:.0f} GB/s over {hp['bytes'] >> 30} GiB "
+                f"({hp['workgroups_per_cu']} workgroups per CU)")
+            cp = bench_hbm_copy_probe(torch)
+            log(f"hbm copy probe: {cp['gbs']:.0f} GB/s read + write "
+                f"({cp['workgroups_per_cu']} workgroups per CU)")
         elif args.only == "mfma-probe":
             mp = bench_mfma_probe(torch)
             log(f"mfma probe: QK operands {mp['qk']:.0f}, PV operands {mp['pv']:.0f}, "
@@ -1118,6 +1172,8 @@ def main(argv=None) -> int:
         f"mix {mp['mix']:.0f} TFLOP/s; prefill = {pre['tflops'] / mp['mix']:.3f} of the mix")
     hp = bench_hbm_probe(torch)
     log(f"hbm read probe: {hp['gbs']:.0f} GB/s over {hp['bytes'] >> 30} GiB")
+    cp = bench_hbm_copy_probe(torch)
+    log(f"hbm copy probe: {cp['gbs']:.0f} GB/s read + write")
     log("c1 ...")
     c1 = bench_prefill_c1(torch, ga, gen)
     log(f"c1: attention {c1['attn_us']:.2f} us ({c1['tflops']:.1f} TFLOP/s), norm "
@@ -1235,7 +1291,14 @@ def main(argv=None) -> int:
         # What a plain streaming read kernel sustains on this GPU (cache-cold, 4 GiB).
         "hbm_read_probe": {"unit": "GB/s", "value": round(hp["gbs"], 1),
                            "frac_of_peak": round(hp["gbs"] / PEAK_HBM_GBS, 4),
+                           "workgroups_per_cu": hp["workgroups_per_cu"],
                            "source": "bench_probes/hbm_read.hip"},
+        # Bytes read + bytes written by a plain streaming copy: the ceiling of the
+        # read-and-write kernels (qk_norm_rope_c3, kv_cache_update_c3).
+        "hbm_copy_probe": {"unit": "GB/s", "value": round(cp["gbs"], 1),
+                           "frac_of_peak": round(cp["gbs"] / PEAK_HBM_GBS, 4),
+                           "workgroups_per_cu": cp["workgroups_per_cu"],
+                           "source": "bench_probes/hbm_copy.hip"},
         "decode": {
             "workload": "c4: Qwen3-32B decode step, 64 Q / 8 KV heads, context 32768, "
                         f"hipGraph x{dec['replays']} of the fused step (norm/RoPE/KV write + "

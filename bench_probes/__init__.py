@@ -7,6 +7,7 @@ for gfx950 into ``bench_probes/libgrout_probe.so``:
 * ``mfma_ceiling.hip``: the sustained v_mfma_f32_32x32x16_f16 rate for
   operand data distributed like the prefill kernel's;
 * ``hbm_read.hip``: the sustained HBM read rate of a plain streaming kernel.
+* ``hbm_copy.hip``: the sustained rate of a plain streaming copy (read + write).
 """
 from __future__ import annotations
 

@@ -2,30 +2,36 @@
 // plain streaming kernel sustains on this GPU, the practical ceiling of the
 // HBM-bound kernels next to the 8 TB/s of the MI355X specification.
 //
-// Every thread reads 16-byte chunks with a grid stride (4 independent loads in
-// flight per iteration) and folds them into one word, written once so the
-// loads cannot be dropped.  bench.py reads a buffer far larger than the
-// 256 MB last-level cache.
+// Every workgroup streams one contiguous region of the buffer; each thread has
+// 16 independent 16-byte non-temporal loads in flight per step (one 64 KB step
+// per workgroup), folded into one word that is written once so the loads
+// cannot be dropped.  With only 4 loads in flight per thread the probe itself
+// was latency-bound (6.0-6.3 TB/s against 7.0-7.2 with 16).  bench.py reads a
+// buffer far larger than the 256 MB last-level cache and keeps the best of a
+// few workgroups-per-CU counts.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace {
 
 typedef uint32_t probe_u4 __attribute__((ext_vector_type(4)));
+constexpr int kInFlight = 16;
 
 __global__ __launch_bounds__(256) void hbm_read_kernel(const probe_u4* __restrict__ src, int64_t n16,
                                                        uint32_t* __restrict__ out) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-    int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * per;
+    const int64_t end = begin + per < n16 ? begin + per : n16;
+    int64_t i = begin + threadIdx.x;
     uint32_t acc = 0;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-        const probe_u4 a = __builtin_nontemporal_load(src + i);
-        const probe_u4 b = __builtin_nontemporal_load(src + i + stride);
-        const probe_u4 c = __builtin_nontemporal_load(src + i + 2 * stride);
-        const probe_u4 d = __builtin_nontemporal_load(src + i + 3 * stride);
-        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+    for (; i + (kInFlight - 1) * 256 < end; i += kInFlight * 256) {
+        probe_u4 v[kInFlight];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) v[u] = __builtin_nontemporal_load(src + i + u * 256);
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
-    for (; i < n16; i += stride) {
+    for (; i < end; i += 256) {
         const probe_u4 a = src[i];
         acc ^= a.x ^ a.y ^ a.z ^ a.w;
     }

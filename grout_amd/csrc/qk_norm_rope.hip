@@ -27,17 +27,19 @@ constexpr int kNormMaxTokens = 8;                // tokens per workgroup (LDS si
 // Prefill launches reserve dynamic LDS so that at most kNormResident
 // workgroups (16 waves) share a CU instead of the 8 that registers and the
 // static 4 KB table allow: fewer concurrent row streams per CU measured
-// 1.5-3% faster at 8192-32768 tokens (c3: 33.2 -> 32.5 us) and no different
-// on grids of at most 4 workgroups per CU.
+// 1.5-3% faster at 8192-32768 tokens (c3: 33.2 -> 32.5 us with the buffers
+// resident in the last-level cache, 42.3 -> 40.9 us with them in HBM) and no
+// different on grids of at most 4 workgroups per CU.
 constexpr int kNormResident = 4;
 constexpr size_t kNormReserveLds =
     160 * 1024 / kNormResident - 2 * kNormMaxTokens * 64 * sizeof(float) - 1024;
 
 // Output stores of the prefill form are non-temporal: q_out and the cache rows
 // are not read again by this kernel, and streaming them past the caches
-// measured 7% faster with the data in HBM (41.3 -> 38.4 us at c3) and no
-// slower with it in the last-level cache.  The decode form keeps ordinary
-// stores: the attention launch that follows reads its rows at once.
+// measured 5% faster with the data in HBM (c3: 40.9 -> 38.9 us), 1% with it
+// in the last-level cache, and 5-30% at 512-2048 tokens.  The decode form
+// keeps ordinary stores: the attention launch that follows reads its rows at
+// once.
 // (Non-temporal loads lose whenever the inputs are still cached from their
 // producer.)
 template <bool kNonTemporal>
