@@ -380,13 +380,11 @@ extern "C" int32_t grout_silu_mul_f16(const uint16_t* gate, const uint16_t* up, 
     return launch_status();
 }
 
-// Residency of the largest GEMVs.  Their launches reserve unused LDS so that at
-// most kGemvResident workgroups share a CU (plain GEMV of >= 2^28 weight
-// elements: lm_head; and the gate_up GEMV with SiLU * up):
-// fewer concurrent row streams per CU.  Measured in the Qwen3-32B token step
-// (one process, graphs alternating, weights loaded non-temporal, 3 chunks in
-// flight): 2 for both 11.54 ms/token; gate_up at 3 11.63, at 1 13.51; lm_head
-// at 3, 4 or uncapped within 0.01 ms of 2.
+// Residency of the largest plain GEMVs (>= 2^28 weight elements: lm_head,
+// 8 rows per workgroup).  Their launches reserve unused LDS so that at most
+// kGemvResident workgroups share a CU: fewer concurrent row streams per CU.
+// With 2 chunks in flight per row this was worth 0.6% of the Qwen3-32B token
+// step; with 3 it is within 0.01 ms of 3, 4 or uncapped.
 constexpr int kGemvResident = 2;
 constexpr size_t gemv_reserve_lds(int resident) {
     return static_cast<size_t>(160 * 1024 / resident - 1024);  // static LDS stays below 1 KB
@@ -399,16 +397,18 @@ extern "C" int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uin
     GROUT_REQUIRE(out != nullptr, GROUT_ERR_NULL_POINTER);
     GROUT_REQUIRE((reinterpret_cast<uintptr_t>(out) & 1u) == 0, GROUT_ERR_ALIGNMENT);
     GROUT_REQUIRE(m >= 1 && k >= 8 && k % 8 == 0 && k <= kGemvMaxK, GROUT_ERR_ARG);
-    // Rows per workgroup: 8 while that still gives >= 4 workgroups per CU
-    // (256 CUs), fewer for short outputs so the grid keeps every CU busy.
-    const int rows = m >= 8 * 1024 ? 8 : m >= 4 * 1024 ? 4 : m >= 2 * 1024 ? 2 : 1;
+    // Rows per workgroup, measured on the Qwen3-32B token step: 2 for the
+    // projections (qkv 10240, o_proj and down 5120 rows: 11.41 against 11.51
+    // ms/token with 8 and 4), 8 only for vocabulary-sized outputs (lm_head at
+    // 2 rows cost 0.1 ms more), 1 below 2048 rows so short outputs still
+    // spread over the CUs.
+    const int rows = m >= 16 * 1024 ? 8 : m >= 2 * 1024 ? 2 : 1;
     const unsigned blocks = static_cast<unsigned>((m + rows - 1) / rows);
     const hipStream_t s = to_hip(stream);
     const dim3 block(kGemvThreads);
     const size_t lds = static_cast<int64_t>(m) * k >= (int64_t{1} << 28) ? gemv_reserve_lds(kGemvResident) : 0;
     switch (rows) {
         case 8: hipLaunchKernelGGL(gemv_f16_kernel<8>, dim3(blocks), block, lds, s, weight, x, out, m, k); break;
-        case 4: hipLaunchKernelGGL(gemv_f16_kernel<4>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
         case 2: hipLaunchKernelGGL(gemv_f16_kernel<2>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
         default: hipLaunchKernelGGL(gemv_f16_kernel<1>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
     }
@@ -422,18 +422,12 @@ extern "C" int32_t grout_gemv_silu_mul_f16(const uint16_t* gate_up, const uint16
     GROUT_REQUIRE(out != nullptr, GROUT_ERR_NULL_POINTER);
     GROUT_REQUIRE((reinterpret_cast<uintptr_t>(out) & 1u) == 0, GROUT_ERR_ALIGNMENT);
     GROUT_REQUIRE(n >= 1 && n <= (1 << 29) && k >= 8 && k % 8 == 0 && k <= kGemvMaxK, GROUT_ERR_ARG);
-    // Weight rows per workgroup as grout_gemv_f16 picks them for the 2n rows.
-    const int rows = 2 * n >= 8 * 1024 ? 8 : 2 * n >= 4 * 1024 ? 4 : 2;
-    const int outs = rows / 2;
-    const unsigned blocks = static_cast<unsigned>((n + outs - 1) / outs);
-    const hipStream_t s = to_hip(stream);
-    const dim3 block(kGemvThreads);
-    switch (rows) {
-        case 8: hipLaunchKernelGGL((gemv_f16_kernel<8, true>), dim3(blocks), block,
-                                   gemv_reserve_lds(kGemvResident), s, gate_up, x, out, n, k, n); break;
-        case 4: hipLaunchKernelGGL((gemv_f16_kernel<4, true>), dim3(blocks), block, 0, s, gate_up, x, out, n, k, n); break;
-        default: hipLaunchKernelGGL((gemv_f16_kernel<2, true>), dim3(blocks), block, 0, s, gate_up, x, out, n, k, n); break;
-    }
+    // One gate row and its up row per workgroup (n workgroups), at full
+    // residency: on the Qwen3-32B token step 11.30 ms/token against 11.41
+    // with 4 + 4 rows and 11.44 with 2 + 2; capping the 2-row workgroups'
+    // residency at 2 or 4 per CU measured 13.71 and 11.81.
+    hipLaunchKernelGGL((gemv_f16_kernel<2, true>), dim3(static_cast<unsigned>(n)), dim3(kGemvThreads),
+                       0, to_hip(stream), gate_up, x, out, n, k, n);
     return launch_status();
 }
 
