@@ -53,6 +53,63 @@ def test_update_matches_oracle(gpu, hkv, MS, S, start, seed):
     assert np.array_equal(dv.cpu().numpy().view(np.uint16), vc.view(np.uint16))
 
 
+@pytest.mark.parametrize("hkv,D,MS,S,start,seed", [
+    (3, 64, 100, 37, 5, 11),     # odd head count, 8 16-byte units per row, ragged last tile
+    (1, 12, 40, 17, 2, 12),      # 8-byte units (head_dim % 8 != 0), 3 per row
+    (5, 8, 33, 33, 0, 13),       # one unit per row, the whole cache
+    (4, 256, 70, 19, 51, 14),    # 32 units per row, the last row written is the cache's last
+    (7, 128, 5000, 4099, 901, 15),  # many tiles, the last one 3 rows
+])
+def test_update_head_dims_and_tiles(gpu, hkv, D, MS, S, start, seed):
+    """The writer's 16-token tiles over every lane layout it supports: head_dim a
+    multiple of 4 (16- or 8-byte units), any head count, seq_len not a multiple
+    of the tile, a sentinel everywhere else in the caches."""
+    import torch
+
+    import grout_amd
+
+    g = rng(seed)
+    nk, nv = normal_f16(g, (S, hkv, D)), normal_f16(g, (S, hkv, D))
+    kc = np.full((hkv, MS, D), 7.0, np.float16)
+    vc = np.full((hkv, MS, D), -3.0, np.float16)
+    dk, dv = torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda()
+    grout_amd.kv_cache_update_seq(torch.from_numpy(nk).cuda(), torch.from_numpy(nv).cuda(), dk,
+                                  dv, start)
+    torch.cuda.synchronize()
+    oracle.kv_cache_update_seq(nk, nv, kc, vc, start)
+    assert np.array_equal(dk.cpu().numpy().view(np.uint16), kc.view(np.uint16))
+    assert np.array_equal(dv.cpu().numpy().view(np.uint16), vc.view(np.uint16))
+
+
+@pytest.mark.parametrize("pos,S", [(60, 20), (0, 33), (79, 1), (80, 17)])
+def test_dynpos_rows_past_the_cache_end(gpu, pos, S):
+    """The device-position form with several rows (the C entry point; the Python
+    mirror keeps the decode path's one row): rows whose slot falls at or past
+    max_seq_len are skipped, the others land as the oracle puts them."""
+    import torch
+
+    import grout_amd
+
+    g = rng(100 + pos + S)
+    hkv, MS, D = 3, 80, 128
+    nk, nv = normal_f16(g, (S, hkv, D)), normal_f16(g, (S, hkv, D))
+    kc = np.full((hkv, MS, D), 7.0, np.float16)
+    vc = np.full((hkv, MS, D), -3.0, np.float16)
+    dk, dv = torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda()
+    tk, tv = torch.from_numpy(nk).cuda(), torch.from_numpy(nv).cuda()
+    dpos = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert grout_amd.lib().grout_kv_cache_update_seq_dynpos(
+        tk.data_ptr(), tv.data_ptr(), dk.data_ptr(), dv.data_ptr(), dpos.data_ptr(), S, hkv, D,
+        MS, st) == 0
+    torch.cuda.synchronize()
+    keep = max(0, min(S, MS - pos))
+    if keep:
+        oracle.kv_cache_update_seq(nk[:keep].copy(), nv[:keep].copy(), kc, vc, pos)
+    assert np.array_equal(dk.cpu().numpy().view(np.uint16), kc.view(np.uint16))
+    assert np.array_equal(dv.cpu().numpy().view(np.uint16), vc.view(np.uint16))
+
+
 def test_dynpos_graph_replay_and_guard(gpu):
     """The device-position form captured once in a hipGraph and replayed at three
     positions (set with grout_set_position_async); a position past the cache
