@@ -341,8 +341,7 @@ def bench_norm(torch, ga, steps, warmup, gen):
     """qk_norm_rope_kv_prefill at c3 shapes (201.3 MB per launch), launches issued from
     a captured graph (no host cost between them).  `ms`: one set of buffers, which the
     256 MB last-level cache partly serves between launches.  `cold_ms`: launches
-    cycling over four sets (805 MB; 384 MB of inputs, as the non-temporal output
-    stores do not stay in that cache), so every launch streams its inputs and outputs
+    cycling over four sets (805 MB), so every launch streams its inputs and outputs
     from and to HBM."""
     hq, hkv, S = 32, 8, 8192
     qw = (1 + 0.1 * torch.randn((D,), device="cuda", generator=gen)).half()

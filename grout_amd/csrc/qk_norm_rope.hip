@@ -30,26 +30,16 @@ constexpr int kNormMaxTokens = 8;                // tokens per workgroup (LDS si
 // 1.5-3% faster at 8192-32768 tokens (c3: 33.2 -> 32.5 us with the buffers
 // resident in the last-level cache, 42.3 -> 40.9 us with them in HBM) and no
 // different on grids of at most 4 workgroups per CU.
+//
+// The outputs are stored with the default policy.  Non-temporal stores made
+// this kernel 5% faster on its own with its data in HBM, but the prefill
+// attention that reads q_out and the cache rows next then finds them outside
+// the last-level cache: the norm + attention pair measured 0.3-0.7% slower
+// (c3 537.7 against 536.3 us, 16384 tokens 2034 against 2020 us, 512 tokens
+// 16.2 against 15.6 us).
 constexpr int kNormResident = 4;
 constexpr size_t kNormReserveLds =
     160 * 1024 / kNormResident - 2 * kNormMaxTokens * 64 * sizeof(float) - 1024;
-
-// Output stores of the prefill form are non-temporal: q_out and the cache rows
-// are not read again by this kernel, and streaming them past the caches
-// measured 5% faster with the data in HBM (c3: 40.9 -> 38.9 us), 1% with it
-// in the last-level cache, and 5-30% at 512-2048 tokens.  The decode form
-// keeps ordinary stores: the attention launch that follows reads its rows at
-// once.
-// (Non-temporal loads lose whenever the inputs are still cached from their
-// producer.)
-template <bool kNonTemporal>
-__device__ __forceinline__ void store_out8(uint16_t* p, half8_t v) {
-    if constexpr (kNonTemporal) {
-        __builtin_nontemporal_store(v, reinterpret_cast<half8_t*>(p));
-    } else {
-        store_half8(p, v);
-    }
-}
 
 template <bool kDevicePos>
 __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_kv_kernel(
@@ -132,15 +122,15 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_kv_kernel(
 
         if (is_q) {
             uint16_t* dst = q_out + (static_cast<int64_t>(s) * num_q_heads + h) * kHeadDim;
-            store_out8<!kDevicePos>(dst + 8 * lane8, ylo);
-            store_out8<!kDevicePos>(dst + 64 + 8 * lane8, yhi);
+            store_half8(dst + 8 * lane8, ylo);
+            store_half8(dst + 64 + 8 * lane8, yhi);
         } else if (static_cast<unsigned>(pos) < static_cast<unsigned>(max_seq_len)) {
             const int64_t slot = (static_cast<int64_t>(kvh) * max_seq_len + pos) * kHeadDim;
-            store_out8<!kDevicePos>(k_cache + slot + 8 * lane8, ylo);
-            store_out8<!kDevicePos>(k_cache + slot + 64 + 8 * lane8, yhi);
+            store_half8(k_cache + slot + 8 * lane8, ylo);
+            store_half8(k_cache + slot + 64 + 8 * lane8, yhi);
             const uint16_t* vsrc = v + (static_cast<int64_t>(s) * num_kv_heads + kvh) * kHeadDim;
-            store_out8<!kDevicePos>(v_cache + slot + 8 * lane8, load_half8(vsrc + 8 * lane8));
-            store_out8<!kDevicePos>(v_cache + slot + 64 + 8 * lane8, load_half8(vsrc + 64 + 8 * lane8));
+            store_u128(v_cache + slot + 8 * lane8, load_u128(vsrc + 8 * lane8));
+            store_u128(v_cache + slot + 64 + 8 * lane8, load_u128(vsrc + 64 + 8 * lane8));
         }
     }
 }
