@@ -15,8 +15,9 @@ fp16 dense MFMA peak, and decode attention GB/s as a fraction of HBM peak.
   also    = c1 (Qwen3-0.6B layer, S=512), c2 (Qwen3-4B decode at context
             4096), c5 (Qwen3-32B prefill at S=32768 with 1% outlier keys,
             unsplit and split-K, then 64 graph-replayed decode steps), the
-            Qwen3-4B decode at context 32768, c3's fused QK norm/RoPE/KV write,
-            the decode-layer ops and the whole Qwen3-32B token step.
+            Qwen3-4B decode at context 32768, c3's fused QK norm/RoPE/KV write
+            and KV suffix writer, the decode-layer ops and the whole Qwen3-32B
+            and Qwen3-4B token steps.
   steady  = c3 once more at the end, after 200 further untimed launches
             (prefill_c3_steady_state): from idle the GPU's power management
             takes ~50 launches to settle, so the headline window (the
@@ -558,13 +559,19 @@ def bench_decode_layer(torch, ga, steps, gen):
     return res
 
 
-def bench_token_step(torch, ga, gen, layers=64, ctx=32768, steps=20):
-    """The whole Qwen3-32B decode token step (hidden 5120, 64 Q / 8 KV heads,
-    intermediate 25600, vocab 151936, `layers` layers) as one hipGraph, every
-    layer's KV cache holding `ctx` tokens: `steps` replays issued back to back
-    from C, each embedding the token the previous one picked.  Random f16
-    weights; bytes per token = every weight matrix + the KV read and written."""
-    hidden, inter, vocab, hq, hkv = 5120, 25600, 151936, 64, 8
+# (layers, hidden, intermediate, Q heads, KV heads) of the token-step legs.
+QWEN3_32B = (64, 5120, 25600, 64, 8)
+QWEN3_4B = (36, 2560, 9728, 32, 8)
+
+
+def bench_token_step(torch, ga, gen, model=QWEN3_32B, ctx=32768, steps=20):
+    """The whole Qwen3 decode token step (`model` = layers, hidden, intermediate,
+    Q / KV heads; vocab 151936) as one hipGraph, every layer's KV cache holding
+    `ctx` tokens: `steps` replays issued back to back from C, each embedding the
+    token the previous one picked.  Random f16 weights; bytes per token = every
+    weight matrix + the KV read and written."""
+    layers, hidden, inter, hq, hkv = model
+    vocab = 151936
     MS = ctx + 1024
     dev = "cuda"
 
@@ -1119,6 +1126,9 @@ def main(argv=None) -> int:
             ts = bench_token_step(torch, ga, gen, steps=args.steps)
             log(f"token step c4 ({ts['layers']} layers, ctx {ts['ctx']}): {ts['ms']:.3f} ms/token, "
                 f"{ts['tokens_per_s']:.1f} tok/s, {ts['gbs']:.0f} GB/s")
+            t4 = bench_token_step(torch, ga, gen, model=QWEN3_4B, steps=args.steps)
+            log(f"token step Qwen3-4B ({t4['layers']} layers, ctx {t4['ctx']}): "
+                f"{t4['ms']:.3f} ms/token, {t4['tokens_per_s']:.1f} tok/s, {t4['gbs']:.0f} GB/s")
         elif args.only == "hbm-probe":
             hp = bench_hbm_probe(torch)
             log(f"hbm read probe: {hp['gbs']:.0f} GB/s over {hp['bytes'] >> 30} GiB "
@@ -1219,6 +1229,9 @@ def main(argv=None) -> int:
     ts = bench_token_step(torch, ga, gen)
     log(f"token step c4 ({ts['layers']} layers, ctx {ts['ctx']}): {ts['ms']:.3f} ms/token, "
         f"{ts['tokens_per_s']:.1f} tok/s, {ts['gbs']:.0f} GB/s")
+    t4 = bench_token_step(torch, ga, gen, model=QWEN3_4B)
+    log(f"token step Qwen3-4B ({t4['layers']} layers, ctx {t4['ctx']}): {t4['ms']:.3f} ms/token, "
+        f"{t4['tokens_per_s']:.1f} tok/s, {t4['gbs']:.0f} GB/s")
 
     log("prefill c3 in the settled power state ...")
     steady = bench_prefill_steady(torch, ga, pre, args.steps)
@@ -1394,6 +1407,15 @@ def main(argv=None) -> int:
             "bytes_per_token": ts["bytes"], "GB/s": round(ts["gbs"], 1),
             "frac_of_hbm_peak": round(ts["gbs"] / PEAK_HBM_GBS, 4),
             "num_splits": ts["num_splits"], "steps": ts["steps"]},
+        "token_step_qwen3_4b": {
+            "workload": f"Qwen3-4B-shaped decode token step (the north star's model: hidden "
+                        f"2560, 32 Q / 8 KV heads, intermediate 9728), {t4['layers']} layers, "
+                        f"every KV cache at context {t4['ctx']}, one hipGraph per token, random "
+                        "f16 weights",
+            "ms_per_token": round(t4["ms"], 3), "tokens_per_s": round(t4["tokens_per_s"], 2),
+            "bytes_per_token": t4["bytes"], "GB/s": round(t4["gbs"], 1),
+            "frac_of_hbm_peak": round(t4["gbs"] / PEAK_HBM_GBS, 4),
+            "num_splits": t4["num_splits"], "steps": t4["steps"]},
         "prefill_c3_steady_state": {
             "note": "the same c3 launches after the bench's other legs and "
                     f"{steady['sustain']} more untimed launches, once the GPU's power "
