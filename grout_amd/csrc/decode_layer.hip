@@ -234,10 +234,29 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_f16_kernel(
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = dot8(wv[u][r], xv[u], acc[r]);
     }
-    for (; c < nchunk; c += kGemvThreads) {  // fewer than kGemvUnroll chunks left
-        const half8_t xv = xc[c];
+    {
+        // Fewer than kGemvUnroll chunks are left; for rows of k <= 4096 that
+        // is the whole row, as the loop above never runs.  Their loads go out
+        // together too, then the dot products run in chunk order (Qwen3-4B
+        // token step 2.557 -> 2.527 ms against one chunk at a time).
+        half8_t wv[kGemvUnroll - 1][R];
+        half8_t xv[kGemvUnroll - 1];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = dot8(__builtin_nontemporal_load(&wr[r][c]), xv, acc[r]);
+        for (int u = 0; u < kGemvUnroll - 1; ++u) {
+            if (c + kGemvThreads * u < nchunk) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) wv[u][r] = __builtin_nontemporal_load(&wr[r][c + kGemvThreads * u]);
+                xv[u] = xc[c + kGemvThreads * u];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < kGemvUnroll - 1; ++u) {
+            if (c + kGemvThreads * u < nchunk) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] = dot8(wv[u][r], xv[u], acc[r]);
+            }
+        }
     }
     const float v = wave_multi_sum<R>(acc, lane);
     constexpr int kStride = kWave / R;
