@@ -400,10 +400,12 @@ extern "C" int32_t grout_silu_mul_f16(const uint16_t* gate, const uint16_t* up, 
 }
 
 // Residency of the largest plain GEMVs (>= 2^28 weight elements: lm_head,
-// 8 rows per workgroup).  Their launches reserve unused LDS so that at most
-// kGemvResident workgroups share a CU: fewer concurrent row streams per CU.
-// With 2 chunks in flight per row this was worth 0.6% of the Qwen3-32B token
-// step; with 3 it is within 0.01 ms of 3, 4 or uncapped.
+// 8 rows per workgroup) with rows longer than 4096: their launches reserve
+// unused LDS so that at most kGemvResident workgroups share a CU, fewer
+// concurrent row streams per CU.  With 2 chunks in flight per row this was
+// worth 0.6% of the Qwen3-32B token step; with 3 it is within 0.01 ms of 3, 4
+// or uncapped.  Short rows (Qwen3-4B's lm_head, k = 2560) run uncapped: their
+// workgroups are short-lived, and the cap cost 21 us of the 4B token step.
 constexpr int kGemvResident = 2;
 constexpr size_t gemv_reserve_lds(int resident) {
     return static_cast<size_t>(160 * 1024 / resident - 1024);  // static LDS stays below 1 KB
@@ -425,7 +427,9 @@ extern "C" int32_t grout_gemv_f16(const uint16_t* weight, const uint16_t* x, uin
     const unsigned blocks = static_cast<unsigned>((m + rows - 1) / rows);
     const hipStream_t s = to_hip(stream);
     const dim3 block(kGemvThreads);
-    const size_t lds = static_cast<int64_t>(m) * k >= (int64_t{1} << 28) ? gemv_reserve_lds(kGemvResident) : 0;
+    const size_t lds = static_cast<int64_t>(m) * k >= (int64_t{1} << 28) && k > 4096
+                           ? gemv_reserve_lds(kGemvResident)
+                           : 0;
     switch (rows) {
         case 8: hipLaunchKernelGGL(gemv_f16_kernel<8>, dim3(blocks), block, lds, s, weight, x, out, m, k); break;
         case 2: hipLaunchKernelGGL(gemv_f16_kernel<2>, dim3(blocks), block, 0, s, weight, x, out, m, k); break;
